@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark: one Wan2.2-5B-shaped DiT block (dim 3072, 24 x 128 heads, FFN
+14336, bf16) on one MI355X through the native HIP path.
+
+Workload "L4680": B=1, 4680 video tokens (RoPE grid 6 x 26 x 30), self
+attention dense over the 4680 tokens, cross attention over a 512-token text
+context whose K/V are precomputed once (WholeLayerBlock.prepare_context).
+A step is one block forward over that batch; inputs are resident in HBM.
+Also reported: the speculative-verify layer slice "Lverify" (4 candidates x
+1560 tokens over a shared 6240-token cached prefix) and a per-stage breakdown.
+
+Prints ONE JSON line (rank 0).  Synthetic data, random-init weights.
+"""
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "wam-egale_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "DiT-block tokens/sec + µs/layer (dim3072 bf16, 1 GPU); % of MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+STAGE_FFN1 = 12
+
+
+def layer_flops(M, D, F, Lc, self_keys, batch=1):
+    """Algorithmic FLOP of one block: 2MNK per GEMM + 4 * (q-k pairs) * D for
+    attention; cross K/V precomputed (not counted)."""
+    R = batch * M
+    gemm = 2 * R * D * (3 * D + D + D + D) + 2 * 2 * R * D * F
+    attn = 4 * R * self_keys * D + 4 * R * Lc * D
+    return gemm, attn
+
+
+def build_block(shape, dev, seed=0):
+    import torch
+    from wam_ops import synthetic
+    from wam_ops.block import TransformerBlock
+    params = synthetic.block_params(shape, seed=seed, device=dev)
+    with torch.device("meta"):
+        blk = TransformerBlock(shape.dim, shape.ffn, shape.heads, cross_attn_norm=True, eps=shape.eps)
+    blk.load_state_dict(params, assign=True)
+    return blk
+
+
+def timed_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def stage_times(lib, call, n_calls, mask):
+    """Average ms per recorded stage over n_calls, from HIP events recorded on
+    the launch stream around each selected stage."""
+    from wam_ops._lib import STAGES
+    timer = lib.wam_timer_create(64 * n_calls, mask)
+    try:
+        for _ in range(n_calls):
+            call(timer)
+        n = 64 * n_calls
+        st = (ctypes.c_int32 * n)()
+        ms = (ctypes.c_float * n)()
+        got = lib.wam_timer_read(timer, st, ms, n)
+        acc = {}
+        for i in range(got):
+            acc.setdefault(STAGES[st[i]], []).append(ms[i])
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+    finally:
+        lib.wam_timer_destroy(timer)
+
+
+def cpu_baseline(shape, seconds_budget=30.0):
+    """The oracle (CPU fp32 restatement of the reference block) on one L4680
+    layer, timed on this host's cores."""
+    import torch
+    from oracle.block import block_forward
+    from wam_ops import synthetic
+    threads = torch.get_num_threads()
+    params = synthetic.block_params(shape, seed=0, device="cpu")
+    params = {k: v.float() for k, v in params.items()}
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4680, (6, 26, 30), context_len=512, seed=1)
+    x, ctx = x.float(), ctx.float()
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)  # warmup
+        first = time.perf_counter() - t0
+        runs = max(1, min(3, int(seconds_budget / max(first, 1e-3)) - 1))
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": 4680 / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one L4680 layer (B=1, 4680 tokens, dim 3072, fp32) through the CPU "
+                      f"oracle, median of {runs} after 1 warmup; {med * 1e3:.0f} ms/layer; "
+                      f"torch threads {threads}, os.cpu_count {os.cpu_count()}, {cpu_model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the block on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured path).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from wam_ops import _lib, synthetic
+    from wam_ops.whole_layer import WholeLayerBlock
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    shape = synthetic.WAN22_5B
+    D, F, M, Lc = shape.dim, shape.ffn, 4680, 512
+
+    blk = build_block(shape, dev)
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, M, (6, 26, 30), context_len=Lc,
+                                                 seed=1, device=dev)
+    layer = WholeLayerBlock(blk)
+    with torch.no_grad():
+        layer.prepare_context(ctx, precompute=True)
+    torch.cuda.synchronize()
+
+    def step(timer=None):
+        with torch.no_grad():
+            return layer(x, ctx, temb, freqs, timer=timer)
+
+    ms = timed_steps(step, args.steps, args.warmup)
+    # Dominant kernel (FFN1 GEMM + GELU): HIP events around its launch on the
+    # launch stream, over the same number of steps.
+    ffn1 = stage_times(lib, step, args.steps, 1 << STAGE_FFN1)["ffn1"]
+    stages = stage_times(lib, step, 3, (1 << len(_lib.STAGES)) - 1)
+
+    gemm, attn = layer_flops(M, D, F, Lc, self_keys=M)
+    flops = gemm + attn
+    ffn1_flops = 2 * M * D * F
+    ffn1_tflops = ffn1_flops / (ffn1 * 1e-3) / 1e12
+    layer_tflops = flops / (ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(M / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "us_per_layer": round(ms * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) activations, N(0,0.02) random-init weights)",
+        "config": {"workload": "L4680: one Wan2.2-5B DiT block, B=1, 4680 tokens (RoPE grid 6x26x30), "
+                               "dim 3072, 24x128 heads, FFN 14336, dense self-attention over 4680, "
+                               "cross-attention over 512 precomputed text K/V",
+                   "tokens": M, "dim": D, "heads": shape.heads, "ffn": F, "context": Lc},
+        "layer_tflops": round(layer_tflops, 1),
+        "layer_frac_of_bf16_peak": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
+        "layer_flop": flops,
+        "roofline": {"bound": "mfma", "kernel": "FFN1 GEMM 4680x14336x3072 + bias + GELU(tanh)",
+                     "achieved": round(ffn1_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel_us": round(ffn1 * 1e3, 1)},
+        "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
+    }
+    if not args.no_verify:
+        # Lverify: 4 candidates x 1560 tokens, each over the shared 6240-token
+        # prefix (pool row 0) plus its own 1560 tokens; read-only cache.
+        Mv, B, prefix = 1560, 4, 6240
+        xv, ctxv, tembv, freqv = synthetic.block_inputs(shape, B, Mv, (2, 26, 30), context_len=Lc,
+                                                        seed=2, device=dev)
+        blk.attn1.attn_caches["pos"] = synthetic.kv_pool(shape, prefix + Mv, prefix, batch=1, device=dev)
+        rows = torch.zeros(B, dtype=torch.int64, device=dev)
+        vlayer = WholeLayerBlock(blk)
+        with torch.no_grad():
+            vlayer.prepare_context(ctxv, precompute=True)
+
+        def vstep():
+            with torch.no_grad():
+                return vlayer(xv, ctxv, tembv, freqv, candidate_cache_rows=rows)
+        # candidate_cache_rows are validated on the host per call, as the reference does
+        vms = timed_steps(vstep, args.steps, args.warmup)
+        g, a = layer_flops(Mv, D, F, Lc, self_keys=prefix + Mv, batch=B)
+        out["lverify"] = {"tokens": B * Mv, "us_per_layer": round(vms * 1e3, 1),
+                          "tokens_per_s": round(B * Mv / (vms * 1e-3), 1),
+                          "tflops": round((g + a) / (vms * 1e-3) / 1e12, 1),
+                          "frac_of_bf16_peak": round((g + a) / (vms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                          "us_30_layers": round(30 * vms * 1e3, 1)}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(shape)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

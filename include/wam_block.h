@@ -1,0 +1,273 @@
+/*
+ * wam_block.h - C ABI of the MI355X (gfx950) Wan DiT block library
+ * (libwam_block.so).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream handle
+ * (passed as void*; NULL is the null stream).  No torch or C++ types cross
+ * this boundary.  All tensors are dense row-major.  Activations are bf16
+ * (2-byte bfloat16); weights are in nn.Linear layout [N_out, K_in], so a
+ * projection computes Y = X * W^T + b.
+ *
+ * Error behaviour: every int-returning entry point returns WAM_OK (0) on
+ * success and a negative WAM_ERR_* code otherwise; wam_last_error() then
+ * holds a message for the calling thread.  Shape/contract violations are
+ * detected on the host before anything is launched (the reference raises
+ * RuntimeError from TORCH_CHECK at the same points:
+ * 算子研究/wam_ops/optimized/csrc/block.cu:320-330).
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   wam_block_forward      <- ext.forward(weights[27], x, context, temb, freq,
+ *                             cache[5], candidate_rows, update, eps[7], debug,
+ *                             fused_ffn1, mode)
+ *                             算子研究/wam_ops/optimized/csrc/block.cu:317-340,348-351
+ *                             and the whole-layer variant
+ *                             算子研究/wam_ops/optimized/csrc/whole_layer.cu:1080-1237
+ *   wam_prepare_context    <- WholeLayerBlock.prepare_context(context, precompute=True)
+ *                             算子研究/wam_ops/optimized/whole_layer.py:41-67
+ *   wam_linear             <- linear(x, w, b) (cuBLASLt, bias epilogue)
+ *                             算子研究/wam_ops/baseline/csrc/gemm.h:35-76, plus the
+ *                             residual/GELU kernels fused into its epilogue
+ *                             算子研究/wam_ops/baseline/csrc/block.cu:90-102,119-129
+ *   wam_ln_modulate        <- norm(x, g, b, eps, rms=false) + table_kernel +
+ *                             modulation_kernel
+ *                             算子研究/wam_ops/baseline/csrc/block.cu:42-89
+ *   wam_rms_rope           <- norm(x, g, {}, eps, rms=true) + rope_kernel
+ *                             算子研究/wam_ops/baseline/csrc/block.cu:42-58,103-118
+ *   wam_attention          <- sdpa(q, k, v) over [history || own] KV
+ *                             算子研究/wam_ops/optimized/csrc/attention_tiles.cu:195-274,
+ *                             with the pool read through a slot list instead of
+ *                             pack_kernel (baseline/csrc/block.cu:213-224)
+ *   wam_kv_layout          <- layout_kernel (slot compaction, eviction, new-slot
+ *                             bookkeeping) 算子研究/wam_ops/baseline/csrc/block.cu:133-200
+ *   wam_kv_commit          <- private_kernel 算子研究/wam_ops/baseline/csrc/block.cu:201-212
+ */
+#ifndef WAM_BLOCK_H
+#define WAM_BLOCK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WAM_ABI_VERSION 1
+
+enum {
+  WAM_OK = 0,
+  WAM_ERR_ARG = -1,   /* contract violation detected on the host */
+  WAM_ERR_HIP = -2,   /* a HIP runtime call failed */
+  WAM_ERR_STATE = -3  /* a device-side contract check failed (see *_info) */
+};
+
+/* Element types; zero (a memset struct) means bf16. */
+enum { WAM_BF16 = 0, WAM_F32 = 1 };
+
+/* Epilogues of wam_linear. */
+enum {
+  WAM_EPI_BIAS = 0,          /* y = bf16(acc + b)                              */
+  WAM_EPI_BIAS_GELU = 1,     /* y = bf16(gelu_tanh(acc + b))                   */
+  WAM_EPI_BIAS_GATE_RES = 2, /* y = bf16(res + (acc + b) * gate[row, col])     */
+  WAM_EPI_BIAS_RES = 3       /* y = bf16(res + (acc + b))                      */
+};
+
+/* Modulation source: mod[b, t, i, :] = table[i, :] + temb[b, t or 0, i, :]
+ * (model.py:751-759; i = 0 shift, 1 scale, 2 gate, 3 c_shift, 4 c_scale,
+ * 5 c_gate).  temb is [B, L, 6, D] with L == 1 (per sample) or L == tokens. */
+typedef struct {
+  const void* table; /* [6, D] */
+  int table_dtype;   /* WAM_F32 | WAM_BF16 */
+  const void* temb;  /* [B, L, 6, D] */
+  int temb_dtype;    /* WAM_F32 | WAM_BF16 */
+  int temb_len;      /* L: 1 or tokens */
+  int tokens;        /* tokens per batch row (M) */
+} wam_modulation;
+
+/* ---------------------------------------------------------------- linear */
+typedef struct {
+  const void* a;     /* [M, K] bf16, row stride lda (elements) */
+  int64_t lda;
+  int M, K;
+  int n_seg;         /* 1..3 output segments (QKV runs as one launch) */
+  int seg_n;         /* columns per segment */
+  const void* w[3];  /* [seg_n, K] bf16 each, row stride ldw */
+  int64_t ldw;
+  const void* bias[3]; /* [seg_n] bf16 each, or NULL */
+  void* out[3];      /* [M, seg_n] bf16 each, row stride ldo */
+  int64_t ldo;
+  int epilogue;      /* WAM_EPI_* */
+  const void* res;   /* residual [M, seg_n], row stride ldr */
+  int64_t ldr;
+  int res_dtype;     /* WAM_BF16 | WAM_F32 */
+  int out_dtype;     /* WAM_BF16 | WAM_F32 (f32 only for the residual epilogues) */
+  wam_modulation gate; /* gate row = mod[b, t, gate_index] for row m = b*tokens+t */
+  int gate_index;
+} wam_linear_args;
+
+int wam_linear(const wam_linear_args* args, void* stream);
+
+/* ----------------------------------------------------------- LayerNorm */
+/* y = bf16(LN(x) * (1 + mod[shift+1]) + mod[shift])   when affine == 0
+ * y = bf16(LN(x) * gamma + beta)                      when affine == 1
+ * LN without affine parameters, fp32 statistics, eps. */
+typedef struct {
+  const void* x; /* [rows, D] bf16 or f32 (x_dtype) */
+  void* y;       /* [rows, D] bf16 */
+  int rows, D;
+  int x_dtype;   /* WAM_BF16 | WAM_F32 */
+  float eps;
+  int affine;
+  const void* gamma; const void* beta; int gb_dtype; /* affine == 1 */
+  wam_modulation mod; int shift_index;              /* affine == 0 */
+} wam_ln_args;
+
+int wam_ln_modulate(const wam_ln_args* args, void* stream);
+
+/* ------------------------------------------------------ RMSNorm + RoPE */
+/* For each of up to two tensors (q, k): y = rope(x * rsqrt(mean(x^2)+eps) * g)
+ * over the full D-wide row (RMSNorm across heads, model.py:325-330,609-612),
+ * RoPE pairs (2j, 2j+1) of every head rotated by freq[bf, t, j]
+ * (model.py:614-623).  In place is allowed (y == x). */
+typedef struct {
+  const void* x[2]; void* y[2]; const void* gamma[2]; float eps[2];
+  int64_t ldx, ldy; /* row strides (elements) */
+  int n_tensors;    /* 1 or 2 */
+  int rows, D, head_dim;
+  const void* freq; /* complex64 [Bf, tokens, head_dim/2] or NULL (no RoPE) */
+  int freq_batch, tokens;
+} wam_rms_rope_args;
+
+int wam_rms_rope(const wam_rms_rope_args* args, void* stream);
+
+/* ------------------------------------------------------------ attention */
+/* O[b, i, h, :] = softmax_j(Q[b,i,h,:] . K_j / sqrt(hd)) V_j over the key list
+ *   j <  n_hist : pool row pool_rows[b] (or b), slot slots[j]
+ *   j >= n_hist : own key (j - n_hist) of own batch row kv_rows[b] (or b)
+ * n_hist is read from device memory (n_hist_dev) so the host never waits for
+ * the slot compaction.  Non-causal, like model.py:37-40. */
+typedef struct {
+  const void* q; int64_t q_bstride, q_rstride;  /* elements */
+  void* o; int64_t o_bstride, o_rstride;
+  int B, Mq, H, head_dim;
+  const void* pool_k; const void* pool_v;
+  int64_t pool_bstride, pool_rstride; int pool_batch;
+  const int32_t* slots; const int32_t* n_hist_dev;
+  const int64_t* pool_rows;
+  const void* k; const void* v; int64_t kv_bstride, kv_rstride; int Mk;
+  const int64_t* kv_rows; int kv_batch;
+  float scale;
+} wam_attention_args;
+
+int wam_attention(const wam_attention_args* args, void* stream);
+
+/* ------------------------------------------------------------- KV pool */
+/* Device-side bookkeeping of the original-mode KV pool (model.py:547-593):
+ *  candidate == 0: evict the oldest ids while fewer than `tokens` slots are
+ *    free (ties by ascending slot), take the first `tokens` free slots, give
+ *    them id = max(valid id) + 1 and is_pred = (update == 1), and set their
+ *    mask to (update != 0) (update 0 is the temporary write whose mask
+ *    restore_cache clears again).
+ *  candidate == 1: read only.
+ * Always: hist_slots = the valid slots before the new ones, in ascending
+ * order, and n_hist their count.  info[0] = n_hist, info[1] = error code
+ * (0 ok, 2 invalid candidate row).  Runs as one workgroup; no host sync. */
+typedef struct {
+  uint8_t* mask; int64_t* ids; uint8_t* is_pred; int pool;
+  int tokens; int update; int candidate;
+  const int64_t* rows; int batch; int pool_batch;
+  int32_t* hist_slots; int32_t* new_slots; int32_t* info;
+} wam_kv_layout_args;
+
+int wam_kv_layout(const wam_kv_layout_args* args, void* stream);
+
+/* Copy the new K/V rows [B, tokens, D] (row stride ld) to pool[b, new_slots[t]]. */
+typedef struct {
+  const void* k; const void* v; int64_t ld;
+  void* pool_k; void* pool_v; int64_t pool_bstride, pool_rstride;
+  const int32_t* new_slots; int B, tokens, D;
+} wam_kv_commit_args;
+
+int wam_kv_commit(const wam_kv_commit_args* args, void* stream);
+
+/* ---------------------------------------------------------------- block */
+/* Weights in the reference order (optimized/native.py:35-49):
+ *  0 scale_shift_table [1,6,D] (f32|bf16)   1,2 norm2 weight/bias (f32|bf16, or NULL)
+ *  3..10 attn1 to_q w,b  to_k w,b  to_v w,b  to_out[0] w,b
+ *  11,12 attn1 norm_q.weight, norm_k.weight
+ *  13..20 attn2 to_q, to_k, to_v, to_out[0] (w,b)   21,22 attn2 norm_q, norm_k
+ *  23,24 ffn.net[0].proj w,b    25,26 ffn.net[2] w,b
+ * eps = [norm1, norm2, norm3, attn1.q, attn1.k, attn2.q, attn2.k]. */
+typedef struct {
+  const void* w[27];
+  int table_dtype; int norm2_dtype;
+  int dim, heads, head_dim, ffn_dim;
+  float eps[7];
+} wam_block_weights;
+
+#define WAM_DEBUG_SLOTS 16
+/* debug[i] (if non-NULL) receives a copy of intermediate i:
+ *  0 modulated1 [R,D]  1 self_q_rope [R,D]  2 self_k_rope [R,D]  3 self_v [R,D]
+ *  4 self_attention [R,D]  5 residual1 [R,D] f32  6 norm2 [R,D]  7 cross_q [R,D]
+ *  8 cross_k [Bc*Lc,D]  9 cross_v [Bc*Lc,D]  10 cross_attention [R,D]
+ *  11 residual2 [R,D] f32  12 modulated3 [R,D]  13 gelu [R,F]  14 output [R,D]
+ * (all bf16 except the two residual-stream tensors, which the block keeps in
+ * fp32 between the input and the output) */
+
+typedef struct {
+  const wam_block_weights* weights;
+  int B, M;                     /* batch rows and tokens per row; R = B*M */
+  const void* x;                /* [B, M, D] bf16 */
+  const void* context;          /* [Bc, Lc, D] bf16; may be NULL when cross_k/v given */
+  int context_batch, context_len;
+  const int64_t* context_rows;  /* [B] context row per batch row, or NULL (= b) */
+  wam_modulation mod;           /* table = weights->w[0] */
+  const void* freq;             /* complex64 [Bf, M, head_dim/2] or NULL */
+  int freq_batch;
+  /* original-mode KV pool; cache_k == NULL means no cache */
+  void* cache_k; void* cache_v; int64_t* cache_id; uint8_t* cache_mask;
+  uint8_t* cache_is_pred; int cache_batch; int pool;
+  const int64_t* candidate_rows; /* [B] or NULL */
+  int update;
+  /* precomputed cross K/V [Bc, Lc, D] (already RMS-normed K); NULL = compute */
+  const void* cross_k; const void* cross_v;
+  void* out;                    /* [B, M, D] bf16 */
+  void* workspace; size_t workspace_bytes;
+  void** debug;                 /* NULL or WAM_DEBUG_SLOTS pointers */
+  void* timer;                  /* NULL or a wam_timer */
+} wam_block_args;
+
+size_t wam_block_workspace_bytes(int B, int M, int dim, int ffn_dim,
+                                 int context_batch, int context_len, int pool);
+int wam_block_forward(const wam_block_args* args, void* stream);
+
+/* Cross K = RMS(ctx Wk^T + bk) * g, V = ctx Wv^T + bv for the context rows
+ * (attn2 of model.py:777-782), written to k_out/v_out [rows, D]. */
+int wam_prepare_context(const wam_block_weights* weights, const void* context,
+                        int rows, void* k_out, void* v_out, void* stream);
+
+/* --------------------------------------------------------------- timing */
+/* Stage timer: pairs of HIP events recorded on the launch stream around
+ * selected stages of wam_block_forward. */
+enum {
+  WAM_STAGE_LN1 = 0, WAM_STAGE_QKV, WAM_STAGE_RMS_ROPE, WAM_STAGE_KV_LAYOUT,
+  WAM_STAGE_SELF_ATTN, WAM_STAGE_SELF_OUT, WAM_STAGE_LN2, WAM_STAGE_CROSS_Q,
+  WAM_STAGE_CROSS_KV, WAM_STAGE_CROSS_ATTN, WAM_STAGE_CROSS_OUT, WAM_STAGE_LN3,
+  WAM_STAGE_FFN1, WAM_STAGE_FFN2, WAM_STAGE_KV_COMMIT, WAM_N_STAGES
+};
+void* wam_timer_create(int capacity, uint32_t stage_mask);
+void wam_timer_reset(void* timer);
+/* Synchronises the recorded events; fills up to max (stage, ms) records. */
+int wam_timer_read(void* timer, int32_t* stages, float* ms, int max);
+void wam_timer_destroy(void* timer);
+
+/* ---------------------------------------------------------------- misc */
+const char* wam_last_error(void);
+int wam_abi_version(void);
+/* sizeof() of the argument struct named `name` (0 if unknown), so bindings
+ * can check their struct layout against the library's. */
+size_t wam_abi_struct_size(const char* name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WAM_BLOCK_H */

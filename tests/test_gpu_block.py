@@ -1,0 +1,167 @@
+"""Whole-block parity: the HIP block (one wam_block_forward call) against the
+CPU fp32 oracle on identical seeded inputs.
+
+Bound (the stated target): max |out - ref| <= 2e-2 and cosine >= 0.9999 for
+the bf16 block against the fp32 reference.
+"""
+import pytest
+import torch
+
+from oracle import kvcache as okv
+from oracle.block import block_forward
+from oracle.metrics import assert_close, compare
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(dim=256, heads=2, ffn=512)
+
+
+def _shape(dim, heads, ffn):
+    from wam_ops.synthetic import BlockShape
+    return BlockShape(dim, heads, ffn)
+
+
+def native_block(params, shape, dev):
+    from wam_ops.block import TransformerBlock
+    blk = TransformerBlock(shape.dim, shape.ffn, shape.heads, cross_attn_norm=True, eps=shape.eps)
+    sd = blk.state_dict()
+    for name, t in params.items():
+        assert name in sd, name
+    with torch.no_grad():
+        for name, mod_param in blk.named_parameters():
+            mod_param.data = params[name].to(dev)
+    return blk.to(dev)
+
+
+def _inputs(shape, B, grid, Lc, seed, per_token=False):
+    from wam_ops import synthetic
+    M = grid[0] * grid[1] * grid[2]
+    return synthetic.block_inputs(shape, B, M, grid, context_len=Lc, context_batch=B, seed=seed,
+                                  per_token_temb=per_token)
+
+
+@pytest.mark.parametrize("cfg,B,grid,Lc,per_token", [
+    (TINY, 1, (3, 4, 5), 16, False),
+    (TINY, 2, (2, 5, 7), 24, True),
+    (dict(dim=3072, heads=24, ffn=14336), 1, (4, 8, 8), 512, False),
+])
+def test_block_vs_fp32_oracle(dev, cfg, B, grid, Lc, per_token):
+    from wam_ops import synthetic
+    shape = _shape(**cfg)
+    params = synthetic.block_params(shape, seed=5)
+    x, ctx, temb, freqs = _inputs(shape, B, grid, Lc, 6, per_token)
+    ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
+    blk = native_block(params, shape, dev)
+    with torch.no_grad():
+        out = blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+    torch.cuda.synchronize()
+    m = assert_close(out.cpu(), ref, max_abs=2e-2, min_cos=0.9999, what=f"block {cfg} B{B} {grid}")
+    print("block parity", cfg, grid, m)
+
+
+def test_block_debug_intermediates(dev):
+    from wam_ops import synthetic
+    shape = _shape(**TINY)
+    params = synthetic.block_params(shape, seed=7)
+    x, ctx, temb, freqs = _inputs(shape, 1, (3, 4, 5), 16, 8)
+    inter = {}
+    block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps, intermediates=inter)
+    from wam_ops.native import NativeBlock
+    blk = native_block(params, shape, dev)
+    with torch.no_grad():
+        dbg = NativeBlock(blk)(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), debug=True)
+    for name in ("modulated1", "residual1", "norm2", "residual2", "modulated3", "gelu", "output"):
+        got = dbg[name].reshape(inter[name].shape).cpu()
+        assert_close(got, inter[name], max_abs=2e-2, min_cos=0.9999, what=name)
+
+
+def test_cache_protocol_sequence(dev):
+    """update 2 -> 1 -> 0 -> candidate rows, outputs and pool state vs the oracle."""
+    from wam_ops import synthetic
+    shape = _shape(**TINY)
+    params = synthetic.block_params(shape, seed=9)
+    blk = native_block(params, shape, dev)
+    P = 150
+    blk.attn1.init_kv_cache("pos", P, shape.heads, shape.head_dim, dev, torch.bfloat16, 1)
+    gcache = blk.attn1.attn_caches["pos"]
+    ocache = okv.new_cache(P, shape.heads, shape.head_dim, 1, torch.float32)
+    grid = (2, 5, 6)
+    for step, upd in enumerate((2, 1, 0, 2, 1)):
+        x, ctx, temb, freqs = _inputs(shape, 1, grid, 16, 20 + step)
+        ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps, cache=ocache,
+                            update_cache=upd)
+        with torch.no_grad():
+            out = blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), update_cache=upd)
+        torch.cuda.synchronize()
+        assert_close(out.cpu(), ref, 2e-2, 0.9999, f"cache step {step} update {upd}")
+        for key in ("mask", "id", "is_pred"):
+            assert torch.equal(gcache[key].cpu(), ocache[key]), (step, key)
+        valid = okv.valid_slots(ocache)
+        assert_close(gcache["k"][:, valid.to(dev)].cpu(), ocache["k"][:, valid], 2e-2, 0.9999, "pool k")
+        assert_close(gcache["v"][:, valid.to(dev)].cpu(), ocache["v"][:, valid], 2e-2, 0.9999, "pool v")
+    # candidate verification: 3 candidates over pool row 0, read only
+    before = {k: v.clone() for k, v in gcache.items()}
+    x, ctx, temb, freqs = _inputs(shape, 3, grid, 16, 40)
+    rows = torch.zeros(3, dtype=torch.int64)
+    ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps, cache=ocache,
+                        update_cache=0, candidate_rows=rows)
+    with torch.no_grad():
+        out = blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), update_cache=0,
+                  candidate_cache_rows=rows.to(dev))
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, 2e-2, 0.9999, "candidate verify")
+    for k in before:
+        assert torch.equal(before[k], gcache[k]), k
+    with pytest.raises(ValueError):
+        with torch.no_grad():
+            blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), update_cache=0,
+                candidate_cache_rows=torch.tensor([0, 1, 0], device=dev))
+
+
+def test_candidates_isolated(dev):
+    """Changing one candidate's tokens leaves every other candidate's output bitwise equal."""
+    from wam_ops import synthetic
+    shape = _shape(**TINY)
+    params = synthetic.block_params(shape, seed=12)
+    blk = native_block(params, shape, dev)
+    blk.attn1.attn_caches["pos"] = synthetic.kv_pool(shape, 120, 90, batch=1, device=dev)
+    x, ctx, temb, freqs = _inputs(shape, 3, (2, 4, 5), 16, 13)
+    x, ctx, temb, freqs = x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev)
+    rows = torch.zeros(3, dtype=torch.int64, device=dev)
+    with torch.no_grad():
+        a = blk(x, ctx, temb, freqs, candidate_cache_rows=rows)
+        x2 = x.clone()
+        x2[1] = -x2[1]
+        b = blk(x2, ctx, temb, freqs, candidate_cache_rows=rows)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[2], b[2])
+    assert not torch.equal(a[1], b[1])
+
+
+def test_whole_layer_precomputed_context(dev):
+    from wam_ops import synthetic
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = _shape(**TINY)
+    params = synthetic.block_params(shape, seed=14)
+    blk = native_block(params, shape, dev)
+    x, ctx, temb, freqs = _inputs(shape, 2, (2, 3, 5), 24, 15)
+    ctx = ctx[:1].expand(2, -1, -1).contiguous()  # CFG-style identical rows
+    x, ctx, temb, freqs = x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev)
+    wl = WholeLayerBlock(blk)
+    with torch.no_grad():
+        base = blk(x, ctx, temb, freqs)
+        wl.prepare_context(ctx, precompute=False)
+        grouped = wl(x, ctx, temb, freqs)
+        wl.prepare_context(ctx, precompute=True)
+        pre = wl(x, ctx, temb, freqs)
+    assert wl.context_rows is not None and wl.context_rows.tolist() == [0, 0]
+    assert torch.equal(base, grouped)
+    assert torch.equal(base, pre)
+
+
+def test_grad_mode_rejected(dev):
+    from wam_ops import synthetic
+    shape = _shape(**TINY)
+    blk = native_block(synthetic.block_params(shape, seed=1), shape, dev)
+    x, ctx, temb, freqs = _inputs(shape, 1, (1, 2, 3), 8, 2)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))

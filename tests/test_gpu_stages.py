@@ -1,0 +1,262 @@
+"""Per-stage parity of the HIP kernels (one C-ABI call each) on the GPU.
+
+References: a plain fp32 torch computation of the same op on the same
+device (GEMM, norms, attention), or the CPU oracle (RoPE, KV pool).
+Tolerances are stated per test; bf16 outputs carry up to half an ulp of
+rounding (2^-9 relative).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import kvcache as okv
+from oracle.block import apply_rope
+from oracle.metrics import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(shape, dev, seed, std=1.0, dtype=torch.bfloat16):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * std).to(dtype)
+
+
+def _ulp_bound(ref, extra=2e-3):
+    """Half an ulp of the largest bf16 output (2^-8 |y|max) plus fp32-order noise."""
+    return 2.0 ** -8 * ref.abs().max().item() + extra
+
+
+def _ref_linear(x, w, b):
+    return x.float() @ w.float().t() + (b.float() if b is not None else 0.0)
+
+
+@pytest.mark.parametrize("M,K,N,nseg", [(1, 64, 128, 1), (300, 256, 384, 1), (77, 512, 256, 3),
+                                        (4680, 3072, 3072, 1), (520, 3072, 3072, 3)])
+def test_linear_bias(dev, M, K, N, nseg):
+    from wam_ops import ops
+    x = _randn((M, K), dev, 1)
+    ws = [_randn((N, K), dev, 10 + i, 0.02) for i in range(nseg)]
+    bs = [_randn((N,), dev, 20 + i, 0.02) for i in range(nseg)]
+    outs = ops.linear(x, ws if nseg > 1 else ws[0], bs if nseg > 1 else bs[0])
+    outs = outs if nseg > 1 else [outs]
+    for o, w, b in zip(outs, ws, bs):
+        ref = _ref_linear(x, w, b)
+        # bf16 output: rounding <= half an ulp = 2^-8 |y|; fp32 accumulation-order noise is far below
+        bound = 2.0 ** -8 * ref.abs().max().item() + 1e-3
+        assert_close(o, ref, max_abs=bound, min_cos=0.99999, what=f"linear {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M", [130, 4680])
+def test_linear_epilogues(dev, M):
+    from wam_ops import ops
+    K, N, D = 1024, 2048, 2048
+    x = _randn((M, K), dev, 2)
+    w = _randn((N, K), dev, 3, 0.05)
+    b = _randn((N,), dev, 4, 0.05)
+    ref = _ref_linear(x, w, b)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_GELU)
+    g = torch.nn.functional.gelu(ref, approximate="tanh")
+    assert_close(y, g, _ulp_bound(g), 0.99999, "gelu")
+    res = _randn((M, N), dev, 5)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_RES, residual=res)
+    assert_close(y, res.float() + ref, _ulp_bound(res.float() + ref), 0.99999, "residual")
+    res32 = _randn((M, N), dev, 5, 1.0, torch.float32)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_RES, residual=res32, out_dtype=torch.float32)
+    assert y.dtype == torch.float32
+    assert_close(y, res32 + ref, 1e-3, 0.999999, "fp32 residual, fp32 out")
+    # gated residual with a per-sample modulation: rows split into 2 samples
+    tokens = M // 2 if M % 2 == 0 else M
+    B = M // tokens
+    table = _randn((1, 6, D), dev, 6, 0.1, torch.float32)
+    temb = _randn((B, 1, 6, D), dev, 7, 0.1, torch.float32)
+    gate = (table[0, 2][None] + temb[:, 0, 2]).repeat_interleave(tokens, 0)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_GATE_RES, residual=res, table=table, temb=temb,
+                   tokens=tokens, gate_index=2)
+    r = res.float() + ref * gate
+    assert_close(y, r, _ulp_bound(r), 0.99999, "gated residual")
+    # per-token bf16 temb
+    tembt = _randn((B, tokens, 6, D), dev, 8, 0.1, torch.bfloat16)
+    gate = (table[0, 5][None, None] + tembt[:, :, 5].float()).reshape(M, D)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_GATE_RES, residual=res, table=table, temb=tembt,
+                   tokens=tokens, gate_index=5)
+    r = res.float() + ref * gate
+    assert_close(y, r, _ulp_bound(r), 0.99999, "gated residual per-token")
+
+
+def test_linear_rejects_bad_shapes(dev):
+    from wam_ops import ops
+    x = _randn((8, 100), dev, 1)
+    w = _randn((128, 100), dev, 2)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        ops.linear(x, w)
+
+
+@pytest.mark.parametrize("B,M,D,L", [(1, 37, 256, 1), (2, 300, 3072, 1), (2, 64, 3072, 64), (1, 5, 1536, 1)])
+def test_ln_modulate(dev, B, M, D, L):
+    from wam_ops import ops
+    x = _randn((B, M, D), dev, 1, 2.0)
+    x = x + _randn((1, 1, D), dev, 9, 1.0)  # non-zero mean
+    table = _randn((1, 6, D), dev, 2, 1 / math.sqrt(D), torch.float32)
+    temb = _randn((B, L, 6, D), dev, 3, 0.1, torch.float32)
+    for shift in (0, 3):
+        y = ops.ln_modulate(x, table, temb, shift, eps=1e-6)
+        y32 = ops.ln_modulate(x.float(), table, temb, shift, eps=1e-6)
+        assert torch.equal(y, y32)  # exact bf16 values read as fp32 give the same result
+        mod = table[None] + temb
+        ref = torch.nn.functional.layer_norm(x.float(), (D,), eps=1e-6) * (1 + mod[:, :, shift + 1]) + mod[:, :, shift]
+        assert_close(y, ref, _ulp_bound(ref), 0.99999, f"ln_modulate shift {shift}")
+    g = _randn((D,), dev, 4, 0.02, torch.float32) + 1
+    bb = _randn((D,), dev, 5, 0.02, torch.float32)
+    y = ops.layer_norm_affine(x, g, bb, eps=1e-6)
+    ref = torch.nn.functional.layer_norm(x.float(), (D,), g, bb, eps=1e-6)
+    assert_close(y, ref, _ulp_bound(ref), 0.99999, "norm2 affine")
+
+
+@pytest.mark.parametrize("B,M,H", [(1, 60, 2), (2, 4680 // 4, 24)])
+def test_rms_rope(dev, B, M, H):
+    from wam_ops import ops, synthetic
+    D = H * 128
+    q = _randn((B, M, D), dev, 1, 3.0)
+    k = _randn((B, M, D), dev, 2, 0.5)
+    gq = _randn((D,), dev, 3, 0.02) + 1
+    gk = _randn((D,), dev, 4, 0.02) + 1
+    f = {60: (3, 4, 5), 1170: (3, 26, 15)}[M]
+    freqs = synthetic.rope_freqs(synthetic.mesh_grid_ids(*f)).to(dev)
+    yq, yk = ops.rms_rope([q, k], [gq, gk], [1e-6, 1e-6], freq=freqs)
+    for y, x, g in ((yq, q, gq), (yk, k, gk)):
+        n = torch.nn.functional.rms_norm(x.float(), (D,), g.float(), 1e-6)
+        ref = apply_rope(n.unflatten(2, (H, 128)), freqs).flatten(2)
+        assert_close(y, ref, _ulp_bound(ref), 0.99999, "rms+rope")
+    # no RoPE (cross q/k), in place
+    q2 = q.clone()
+    ops.rms_rope([q2], [gq], [1e-6], out=[q2])
+    ref = torch.nn.functional.rms_norm(q.float(), (D,), gq.float(), 1e-6)
+    assert_close(q2, ref, _ulp_bound(ref), 0.99999, "rms in place")
+
+
+def _ref_attn(q, k, v):
+    return torch.nn.functional.scaled_dot_product_attention(
+        q.float().transpose(1, 2), k.float().transpose(1, 2), v.float().transpose(1, 2)).transpose(1, 2)
+
+
+@pytest.mark.parametrize("B,Mq,Mk,H", [(1, 1, 1, 1), (1, 100, 37, 2), (2, 129, 200, 3),
+                                       (1, 4680, 512, 24), (1, 1560, 1560, 24)])
+def test_attention_plain(dev, B, Mq, Mk, H):
+    from wam_ops import ops
+    q = _randn((B, Mq, H, 128), dev, 1)
+    k = _randn((B, Mk, H, 128), dev, 2)
+    v = _randn((B, Mk, H, 128), dev, 3)
+    o = ops.attention(q, k, v)
+    assert_close(o, _ref_attn(q, k, v), 2e-2, 0.9999, f"attention {B}x{Mq}x{Mk}x{H}")
+
+
+def test_attention_strided_and_broadcast(dev):
+    from wam_ops import ops
+    B, M, H = 2, 70, 2
+    qkv = _randn((B, M, 3, H, 128), dev, 1)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    o = ops.attention(q, k, v)
+    assert_close(o, _ref_attn(q, k, v), 2e-2, 0.9999, "strided qkv")
+    kc = _randn((1, 33, H, 128), dev, 4)
+    vc = _randn((1, 33, H, 128), dev, 5)
+    o = ops.attention(q, kc, vc)  # one context row for both samples
+    assert_close(o, _ref_attn(q, kc.expand(B, -1, -1, -1), vc.expand(B, -1, -1, -1)), 2e-2, 0.9999, "broadcast")
+    rows = torch.tensor([0, 0], dtype=torch.int64, device=dev)
+    o = ops.attention(q, k, v, kv_rows=rows)
+    assert_close(o, _ref_attn(q, k[:1].expand(B, -1, -1, -1), v[:1].expand(B, -1, -1, -1)), 2e-2, 0.9999, "kv_rows")
+
+
+@pytest.mark.parametrize("B,Mq,P,nvalid,Bp,candidate", [(1, 50, 300, 170, 1, False),
+                                                        (2, 64, 500, 321, 2, False),
+                                                        (4, 33, 400, 250, 2, True),
+                                                        (4, 1560, 7800, 6240, 1, True)])
+def test_attention_history(dev, B, Mq, P, nvalid, Bp, candidate):
+    from wam_ops import ops
+    H = 2 if Mq < 1000 else 24
+    q = _randn((B, Mq, H, 128), dev, 1)
+    k = _randn((B, Mq, H, 128), dev, 2)
+    v = _randn((B, Mq, H, 128), dev, 3)
+    pk = _randn((Bp, P, H, 128), dev, 4)
+    pv = _randn((Bp, P, H, 128), dev, 5)
+    g = torch.Generator().manual_seed(6)
+    slots = torch.randperm(P, generator=g)[:nvalid].sort().values
+    slots_d = slots.to(torch.int32).to(dev)
+    n = torch.tensor([nvalid], dtype=torch.int32, device=dev)
+    rows = torch.tensor([i % Bp for i in range(B)], dtype=torch.int64, device=dev) if candidate else None
+    o = ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots_d, n_hist=n, pool_rows=rows)
+    r = rows if candidate else torch.arange(B, device=dev)
+    hk = pk[:, slots.to(dev)].index_select(0, r)
+    hv = pv[:, slots.to(dev)].index_select(0, r)
+    ref = _ref_attn(q, torch.cat([hk, k], 1), torch.cat([hv, v], 1))
+    assert_close(o, ref, 2e-2, 0.9999, "history attention")
+
+
+def _cache_pair(P, H, seed, dev, prefix_chunks):
+    """Identical CPU (oracle) and GPU pools after committing some chunks."""
+    c = okv.new_cache(P, H, 128, 1, torch.bfloat16)
+    g = torch.Generator().manual_seed(seed)
+    for n, upd in prefix_chunks:
+        kk = torch.randn(1, n, H, 128, generator=g).bfloat16()
+        okv.update_cache(c, kk, kk, is_pred=(upd == 1))
+    return c, {k: v.to(dev) for k, v in c.items()}
+
+
+@pytest.mark.parametrize("P,chunks,tokens,update", [
+    (100, [(30, 2), (30, 1)], 20, 0),
+    (100, [(30, 2), (30, 1)], 20, 1),
+    (100, [(40, 2), (40, 2)], 40, 2),      # evicts 20 of the oldest chunk
+    (64, [(32, 2), (32, 1)], 48, 1),       # evicts a whole chunk and part of the next
+    (3000, [(1000, 2), (1000, 1), (900, 2)], 1000, 0),
+])
+def test_kv_layout_matches_oracle(dev, P, chunks, tokens, update):
+    from wam_ops import ops
+    H = 1
+    cpu, gpu = _cache_pair(P, H, 11, dev, chunks)
+    # oracle: slots chosen by update_cache, history = valid minus the new slots
+    ref = okv.clone_cache(cpu)
+    kk = torch.zeros(1, tokens, H, 128, dtype=torch.bfloat16)
+    new = okv.update_cache(ref, kk, kk, is_pred=(update == 1))
+    valid_after = okv.valid_slots(ref)
+    hist_ref = [s for s in valid_after.tolist() if s not in set(new.tolist())]
+    if update == 0:
+        okv.restore_cache(ref, new)
+    hist, newslots, info = ops.kv_layout(gpu, tokens, update)
+    torch.cuda.synchronize()
+    n = int(info[0])
+    assert int(info[1]) == 0
+    assert hist[:n].cpu().tolist() == hist_ref
+    assert newslots[:tokens].cpu().tolist() == new.tolist()
+    for key in ("mask", "id", "is_pred"):
+        assert torch.equal(gpu[key].cpu(), ref[key]), key
+
+
+def test_kv_layout_candidate_read_only(dev):
+    from wam_ops import ops
+    cpu, gpu = _cache_pair(50, 1, 3, dev, [(20, 2), (10, 1)])
+    before = {k: v.clone() for k, v in gpu.items()}
+    rows = torch.tensor([0, 0, 0], dtype=torch.int64, device=dev)
+    hist, _, info = ops.kv_layout(gpu, 5, 0, candidate_rows=rows)
+    torch.cuda.synchronize()
+    assert int(info[1]) == 0 and int(info[0]) == 30
+    assert hist[:30].cpu().tolist() == okv.valid_slots(cpu).tolist()
+    for k in before:
+        assert torch.equal(before[k], gpu[k])
+    bad = torch.tensor([0, 1, 0], dtype=torch.int64, device=dev)
+    _, _, info = ops.kv_layout(gpu, 5, 0, candidate_rows=bad)
+    torch.cuda.synchronize()
+    assert int(info[1]) == 2
+
+
+def test_kv_commit(dev):
+    from wam_ops import ops
+    P, H, M = 40, 2, 7
+    cache = {"k": torch.zeros(2, P, H, 128, dtype=torch.bfloat16, device=dev),
+             "v": torch.zeros(2, P, H, 128, dtype=torch.bfloat16, device=dev)}
+    k = _randn((2, M, H * 128), dev, 1)
+    v = _randn((2, M, H * 128), dev, 2)
+    slots = torch.tensor([3, 9, 10, 11, 20, 30, 39], dtype=torch.int32, device=dev)
+    ops.kv_commit(cache, k, v, slots)
+    s = slots.long()
+    assert torch.equal(cache["k"][:, s].flatten(2), k)
+    assert torch.equal(cache["v"][:, s].flatten(2), v)

@@ -1,0 +1,214 @@
+// Original-mode KV pool bookkeeping on the device (no host synchronisation).
+//
+// Pool state (model.py:417-434): k, v [B_cfg, P, H, hd] bf16, id [P] int64,
+// mask [P] bool, is_pred [P] bool.  One call of the self-attention with a
+// cache (model.py:662-686) does:
+//   allocate_slots (model.py:547-566): if fewer than `tokens` slots are free,
+//     evict the valid slots with the smallest ids (the reference sorts with
+//     torch.argsort; ties are broken here by ascending slot, the order a
+//     stable sort gives), then take the first `tokens` free slots;
+//   update_cache (model.py:577-590): new id = max(valid id) + 1 (0 if none),
+//     write K/V, mask = True, id = new id, is_pred = (update == 1);
+//   attention over every valid slot in ascending slot order;
+//   restore_cache for update == 0 (model.py:592-593, 683-685): mask = False.
+// Candidate verification (model.py:624-660) is read only.
+//
+// This kernel does the index work of all of that; the K/V rows themselves are
+// written by wam_kv_commit, and attention reads the history through
+// hist_slots (the valid slots other than the new ones) plus the new rows
+// straight from the projection output.  Softmax over a key set does not
+// depend on key order, so [history || own] equals the reference's slot order
+// up to fp32 summation order.  The native reference does the same work in
+// layout_kernel / private_kernel / restore_kernel,
+// 算子研究/wam_ops/baseline/csrc/block.cu:133-227.
+#include "wam_common.h"
+
+namespace wam {
+
+constexpr int kLayoutThreads = 1024;
+constexpr int kLayoutWaves = kLayoutThreads / 64;
+
+__device__ inline int block_excl_scan(int v, int* sh, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sh[w] = x;
+  __syncthreads();
+  int off = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kLayoutWaves; ++i) {
+    const int t = sh[i];
+    off += i < w ? t : 0;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + x - v;
+}
+
+__device__ inline int block_sum(int v, int* sh) {
+  int tot;
+  block_excl_scan(v, sh, &tot);
+  return tot;
+}
+
+__device__ inline long long block_reduce_ll(long long v, bool take_max, long long* sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const long long y = __shfl_xor(v, o, 64);
+    v = take_max ? (y > v ? y : v) : (y < v ? y : v);
+  }
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  long long r = sh[0];
+#pragma unroll
+  for (int i = 1; i < kLayoutWaves; ++i) {
+    const long long t = sh[i];
+    r = take_max ? (t > r ? t : r) : (t < r ? t : r);
+  }
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout_args a) {
+  __shared__ int sh_i[kLayoutWaves];
+  __shared__ long long sh_ll[kLayoutWaves];
+  const int tid = threadIdx.x, P = a.pool;
+  int error = 0;
+  if (a.candidate) {
+    int bad = 0;
+    for (int b = tid; b < a.batch; b += kLayoutThreads)
+      bad |= (a.rows[b] < 0 || a.rows[b] >= a.pool_batch);
+    if (block_sum(bad, sh_i) != 0) error = 2;
+  } else {
+    // Eviction of the oldest ids (allocate_slots).
+    int nfree = 0;
+    for (int c = 0; c < P; c += kLayoutThreads) {
+      const int i = c + tid;
+      nfree += block_sum(i < P && !a.mask[i], sh_i);
+    }
+    int need = a.tokens - nfree;
+    while (need > 0) {
+      long long mn = 0x7fffffffffffffffLL;
+      for (int c = 0; c < P; c += kLayoutThreads) {
+        const int i = c + tid;
+        const long long v = (i < P && a.mask[i]) ? (long long)a.ids[i] : 0x7fffffffffffffffLL;
+        const long long r = block_reduce_ll(v, false, sh_ll);
+        mn = r < mn ? r : mn;
+      }
+      int base = 0;
+      for (int c = 0; c < P; c += kLayoutThreads) {
+        const int i = c + tid;
+        const int f = (i < P && a.mask[i] && a.ids[i] == mn) ? 1 : 0;
+        int tot;
+        const int pos = block_excl_scan(f, sh_i, &tot) + base;
+        if (f && pos < need) {
+          a.mask[i] = 0;
+          a.ids[i] = -1;
+        }
+        base += tot;
+      }
+      need -= base;
+      __syncthreads();
+      if (base == 0) {  // no valid slot left to evict: the host checks make this unreachable
+        error = 1;
+        break;
+      }
+    }
+  }
+  // Next id over the (post-eviction) valid slots (_next_cache_id).
+  long long next = -1;
+  if (!a.candidate) {
+    for (int c = 0; c < P; c += kLayoutThreads) {
+      const int i = c + tid;
+      const long long v = (i < P && a.mask[i]) ? (long long)a.ids[i] : -1LL;
+      const long long r = block_reduce_ll(v, true, sh_ll);
+      next = r > next ? r : next;
+    }
+    next += 1;
+  }
+  // History list and new slots, both in ascending slot order.
+  int base_v = 0, base_f = 0;
+  for (int c = 0; c < P; c += kLayoutThreads) {
+    const int i = c + tid;
+    const int valid = (i < P && a.mask[i]) ? 1 : 0;
+    const int fr = (!a.candidate && i < P && !valid) ? 1 : 0;
+    int tv, tf;
+    const int pv = block_excl_scan(valid, sh_i, &tv) + base_v;
+    const int pf = block_excl_scan(fr, sh_i, &tf) + base_f;
+    if (valid) a.hist_slots[pv] = i;
+    if (fr && pf < a.tokens) {
+      a.new_slots[pf] = i;
+      a.mask[i] = a.update != 0 ? 1 : 0;
+      a.ids[i] = next;
+      a.is_pred[i] = a.update == 1 ? 1 : 0;
+    }
+    base_v += tv;
+    base_f += tf;
+  }
+  if (tid == 0) {
+    a.info[0] = base_v;
+    a.info[1] = error;
+  }
+}
+
+int kv_layout(const wam_kv_layout_args* a, hipStream_t s) {
+  WAM_REQUIRE(a != nullptr, "wam_kv_layout: null args");
+  WAM_REQUIRE(a->mask && a->ids && a->is_pred && a->hist_slots && a->info,
+              "wam_kv_layout: null pool state");
+  WAM_REQUIRE(a->pool > 0, "wam_kv_layout: empty pool");
+  if (a->candidate) {
+    WAM_REQUIRE(a->rows != nullptr && a->batch > 0 && a->pool_batch > 0,
+                "wam_kv_layout: candidate mode needs rows");
+    WAM_REQUIRE(a->update == 0, "candidate verification requires existing read-only KV (update 0)");
+  } else {
+    WAM_REQUIRE(a->new_slots != nullptr, "wam_kv_layout: null new_slots");
+    WAM_REQUIRE(a->update >= 0 && a->update <= 2, "wam_kv_layout: update must be 0, 1 or 2");
+    WAM_REQUIRE(a->tokens >= 1 && a->tokens <= a->pool,
+                "wam_kv_layout: %d new tokens do not fit a pool of %d slots", a->tokens, a->pool);
+  }
+  hipLaunchKernelGGL(kv_layout_kernel, dim3(1), dim3(kLayoutThreads), 0, s, *a);
+  WAM_LAUNCHED("kv_layout_kernel");
+  return WAM_OK;
+}
+
+__global__ __launch_bounds__(256) void kv_commit_kernel(wam_kv_commit_args a) {
+  const int chunks = a.D >> 3;
+  const int64_t n = (int64_t)a.B * a.tokens * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t row = i / chunks;
+    const int c = (int)(i - row * chunks);
+    const int64_t b = row / a.tokens, t = row - b * a.tokens;
+    const int64_t src = row * a.ld + c * 8;
+    const int64_t dst = b * a.pool_bstride + (int64_t)a.new_slots[t] * a.pool_rstride + c * 8;
+    st_bf16x8(static_cast<bf16*>(a.pool_k) + dst, ld_bf16x8(static_cast<const bf16*>(a.k) + src));
+    st_bf16x8(static_cast<bf16*>(a.pool_v) + dst, ld_bf16x8(static_cast<const bf16*>(a.v) + src));
+  }
+}
+
+int kv_commit(const wam_kv_commit_args* a, hipStream_t s) {
+  WAM_REQUIRE(a != nullptr && a->k && a->v && a->pool_k && a->pool_v && a->new_slots,
+              "wam_kv_commit: null pointer");
+  WAM_REQUIRE(a->D % 8 == 0 && a->ld % 8 == 0 && a->pool_rstride % 8 == 0 && a->pool_bstride % 8 == 0,
+              "wam_kv_commit: 16-byte alignment contract");
+  const int64_t n = (int64_t)a->B * a->tokens * (a->D / 8);
+  if (n == 0) return WAM_OK;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(kv_commit_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, *a);
+  WAM_LAUNCHED("kv_commit_kernel");
+  return WAM_OK;
+}
+
+}  // namespace wam
+
+extern "C" int wam_kv_layout(const wam_kv_layout_args* args, void* stream) {
+  return wam::kv_layout(args, static_cast<hipStream_t>(stream));
+}
+extern "C" int wam_kv_commit(const wam_kv_commit_args* args, void* stream) {
+  return wam::kv_commit(args, static_cast<hipStream_t>(stream));
+}

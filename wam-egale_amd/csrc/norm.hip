@@ -1,0 +1,204 @@
+// Row-reduction kernels: LayerNorm fused with AdaLN modulation, and the
+// across-heads RMSNorm fused with 3D RoPE.  One wave64 owns one row; the row
+// stays in registers between the statistics and the normalisation, so each
+// row is read from HBM once and written once.
+//
+// LayerNorm+modulate follows model.py:761-763 / 786-788 (norm1/norm3:
+// FP32LayerNorm without affine, then x*(1+scale)+shift, cast to bf16) and
+// model.py:775-776 (norm2: FP32LayerNorm with fp32 affine).  The reference's
+// native equivalents are norm/modulation_kernel/table_kernel in
+// 算子研究/wam_ops/baseline/csrc/block.cu:42-89.
+//
+// RMSNorm+RoPE follows model.py:609-623: RMSNorm over the full D-wide row
+// (all heads), times the affine weight, then the complex rotation of pair
+// (2j, 2j+1) of every head by freq[t, j]; baseline/csrc/block.cu:103-118.
+#include "wam_common.h"
+
+namespace wam {
+
+// ------------------------------------------------------------- LayerNorm
+template <int CH>  // 16-byte chunks per lane (D <= CH * 512)
+__global__ __launch_bounds__(256) void ln_modulate_kernel(wam_ln_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int D = a.D, nch = D >> 3;
+  float v[CH][8];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch < nch) {
+      if (a.x_dtype == WAM_F32) {
+        const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + row * D + ch * 8);
+        const float4 p0 = xp[0], p1 = xp[1];
+        v[c][0] = p0.x; v[c][1] = p0.y; v[c][2] = p0.z; v[c][3] = p0.w;
+        v[c][4] = p1.x; v[c][5] = p1.y; v[c][6] = p1.z; v[c][7] = p1.w;
+      } else {
+        const bf16x8 t = ld_bf16x8(static_cast<const bf16*>(a.x) + row * D + ch * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = static_cast<float>(t[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[c][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[c][e] = 0.f;
+    }
+  }
+  const float mean = wave_sum(s) / D;
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float d = v[c][e] - mean; q += d * d; }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
+  bf16* y = static_cast<bf16*>(a.y) + row * D;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch >= nch) continue;
+    const int d0 = ch * 8;
+    float mul[8], add[8];
+    if (a.affine) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        mul[e] = ld_scalar(a.gamma, a.gb_dtype, d0 + e);
+        add[e] = ld_scalar(a.beta, a.gb_dtype, d0 + e);
+      }
+    } else {
+      ld_mod8(a.mod, D, row, a.shift_index, d0, add);
+      ld_mod8(a.mod, D, row, a.shift_index + 1, d0, mul);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mul[e] += 1.f;
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[e] + add[e]);
+    st_bf16x8(y + d0, o);
+  }
+}
+
+int ln_modulate(const wam_ln_args* a, hipStream_t s) {
+  WAM_REQUIRE(a != nullptr, "wam_ln_modulate: null args");
+  WAM_REQUIRE(a->rows >= 0 && a->D > 0 && a->D % 8 == 0 && a->D <= 4096,
+              "wam_ln_modulate: D=%d must be a multiple of 8 and <= 4096", a->D);
+  WAM_REQUIRE(a->x && a->y, "wam_ln_modulate: null x/y");
+  WAM_REQUIRE(a->x_dtype == WAM_BF16 || a->x_dtype == WAM_F32, "wam_ln_modulate: x dtype");
+  if (a->affine) {
+    WAM_REQUIRE(a->gamma && a->beta, "wam_ln_modulate: affine needs gamma and beta");
+  } else {
+    WAM_REQUIRE(a->mod.table && a->mod.temb && a->mod.tokens > 0 &&
+                (a->mod.temb_len == 1 || a->mod.temb_len == a->mod.tokens) &&
+                a->rows % a->mod.tokens == 0 && (a->shift_index == 0 || a->shift_index == 3),
+                "wam_ln_modulate: modulation contract (shift index %d)", a->shift_index);
+  }
+  if (a->rows == 0) return WAM_OK;
+  const dim3 grid((a->rows + 3) / 4), block(256);
+  const int ch = (a->D / 8 + 63) / 64;
+  if (ch <= 1) hipLaunchKernelGGL(ln_modulate_kernel<1>, grid, block, 0, s, *a);
+  else if (ch <= 2) hipLaunchKernelGGL(ln_modulate_kernel<2>, grid, block, 0, s, *a);
+  else if (ch <= 3) hipLaunchKernelGGL(ln_modulate_kernel<3>, grid, block, 0, s, *a);
+  else if (ch <= 6) hipLaunchKernelGGL(ln_modulate_kernel<6>, grid, block, 0, s, *a);
+  else hipLaunchKernelGGL(ln_modulate_kernel<8>, grid, block, 0, s, *a);
+  WAM_LAUNCHED("ln_modulate_kernel");
+  return WAM_OK;
+}
+
+// ------------------------------------------------------- RMSNorm + RoPE
+template <int CH>
+__global__ __launch_bounds__(256) void rms_rope_kernel(wam_rms_rope_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t job = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (job >= (int64_t)a.rows * a.n_tensors) return;
+  const int tsel = (int)(job % a.n_tensors);
+  const int64_t row = job / a.n_tensors;
+  const int D = a.D, nch = D >> 3;
+  const bf16* x = static_cast<const bf16*>(tsel ? a.x[1] : a.x[0]) + row * a.ldx;
+  bf16* y = static_cast<bf16*>(tsel ? a.y[1] : a.y[0]) + row * a.ldy;
+  const bf16* g = static_cast<const bf16*>(tsel ? a.gamma[1] : a.gamma[0]);
+  const float eps = tsel ? a.eps[1] : a.eps[0];
+  float v[CH][8];
+  float q = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch < nch) {
+      bf16x8 t = ld_bf16x8(x + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { v[c][e] = static_cast<float>(t[e]); q += v[c][e] * v[c][e]; }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / D + eps);
+  const float2* f = nullptr;
+  if (a.freq) {
+    const int64_t b = row / a.tokens, t = row - b * a.tokens;
+    const int64_t fb = a.freq_batch == 1 ? 0 : b;
+    f = static_cast<const float2*>(a.freq) + (fb * a.tokens + t) * (a.head_dim / 2);
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch >= nch) continue;
+    const int d0 = ch * 8;
+    bf16x8 gv = ld_bf16x8(g + d0);
+    float n[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) n[e] = v[c][e] * rstd * static_cast<float>(gv[e]);
+    if (f) {
+      const int j0 = (d0 % a.head_dim) >> 1;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const float2 z = f[j0 + (e >> 1)];
+        const float re = n[e], im = n[e + 1];
+        n[e] = re * z.x - im * z.y;
+        n[e + 1] = re * z.y + im * z.x;
+      }
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>(n[e]);
+    st_bf16x8(y + d0, o);
+  }
+}
+
+int rms_rope(const wam_rms_rope_args* a, hipStream_t s) {
+  WAM_REQUIRE(a != nullptr, "wam_rms_rope: null args");
+  WAM_REQUIRE(a->n_tensors == 1 || a->n_tensors == 2, "wam_rms_rope: n_tensors must be 1 or 2");
+  WAM_REQUIRE(a->D > 0 && a->D % 8 == 0 && a->D <= 4096, "wam_rms_rope: D=%d unsupported", a->D);
+  WAM_REQUIRE(a->ldx % 8 == 0 && a->ldy % 8 == 0 && a->ldx >= a->D && a->ldy >= a->D,
+              "wam_rms_rope: row strides must be >= D and 16-byte aligned");
+  for (int i = 0; i < a->n_tensors; ++i)
+    WAM_REQUIRE(a->x[i] && a->y[i] && a->gamma[i], "wam_rms_rope: null tensor %d", i);
+  if (a->freq) {
+    WAM_REQUIRE(a->head_dim > 0 && a->head_dim % 8 == 0 && a->D % a->head_dim == 0,
+                "wam_rms_rope: head_dim=%d must divide D and be a multiple of 8", a->head_dim);
+    WAM_REQUIRE(a->tokens > 0 && a->rows % a->tokens == 0 && a->freq_batch >= 1 &&
+                (a->freq_batch == 1 || a->freq_batch == a->rows / a->tokens),
+                "wam_rms_rope: freq batch %d / tokens %d contract", a->freq_batch, a->tokens);
+  }
+  if (a->rows == 0) return WAM_OK;
+  const int64_t jobs = (int64_t)a->rows * a->n_tensors;
+  const dim3 grid((unsigned)((jobs + 3) / 4)), block(256);
+  const int ch = (a->D / 8 + 63) / 64;
+  if (ch <= 1) hipLaunchKernelGGL(rms_rope_kernel<1>, grid, block, 0, s, *a);
+  else if (ch <= 2) hipLaunchKernelGGL(rms_rope_kernel<2>, grid, block, 0, s, *a);
+  else if (ch <= 3) hipLaunchKernelGGL(rms_rope_kernel<3>, grid, block, 0, s, *a);
+  else if (ch <= 6) hipLaunchKernelGGL(rms_rope_kernel<6>, grid, block, 0, s, *a);
+  else hipLaunchKernelGGL(rms_rope_kernel<8>, grid, block, 0, s, *a);
+  WAM_LAUNCHED("rms_rope_kernel");
+  return WAM_OK;
+}
+
+}  // namespace wam
+
+extern "C" int wam_ln_modulate(const wam_ln_args* args, void* stream) {
+  return wam::ln_modulate(args, static_cast<hipStream_t>(stream));
+}
+extern "C" int wam_rms_rope(const wam_rms_rope_args* args, void* stream) {
+  return wam::rms_rope(args, static_cast<hipStream_t>(stream));
+}

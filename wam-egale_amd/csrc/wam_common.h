@@ -1,0 +1,128 @@
+// Shared device/host helpers of libwam_block.so (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include "../../include/wam_block.h"
+
+namespace wam {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- host side
+void set_error(const char* fmt, ...);
+
+#define WAM_REQUIRE(cond, ...)              \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::wam::set_error(__VA_ARGS__);        \
+      return WAM_ERR_ARG;                   \
+    }                                       \
+  } while (0)
+
+#define WAM_HIP(call)                                                        \
+  do {                                                                       \
+    hipError_t e_ = (call);                                                  \
+    if (e_ != hipSuccess) {                                                  \
+      ::wam::set_error("%s failed: %s", #call, hipGetErrorString(e_));       \
+      return WAM_ERR_HIP;                                                    \
+    }                                                                        \
+  } while (0)
+
+#define WAM_LAUNCHED(name)                                                   \
+  do {                                                                       \
+    hipError_t e_ = hipGetLastError();                                       \
+    if (e_ != hipSuccess) {                                                  \
+      ::wam::set_error("launch of %s failed: %s", name, hipGetErrorString(e_)); \
+      return WAM_ERR_HIP;                                                    \
+    }                                                                        \
+  } while (0)
+
+#define WAM_TRY(expr)            \
+  do {                           \
+    int rc_ = (expr);            \
+    if (rc_ != WAM_OK) return rc_; \
+  } while (0)
+
+// Workgroup i is dispatched to XCD i % 8 on MI355X.  Remap so that each XCD
+// receives one contiguous range of logical ids (bijective for any n).
+__host__ __device__ inline int xcd_remap(int i, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int x = i & 7, k = i >> 3;
+  return x * q + (x < r ? x : r) + k;
+}
+
+// --------------------------------------------------------------- device side
+__device__ inline float ld_scalar(const void* p, int dtype, int64_t i) {
+  return dtype == WAM_F32 ? static_cast<const float*>(p)[i]
+                          : static_cast<float>(static_cast<const bf16*>(p)[i]);
+}
+
+// Force a wave-uniform pointer into SGPRs (the compiler cannot always prove
+// uniformity of pointers selected from kernel arguments).
+template <class T>
+__device__ inline T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+// Raw buffer resource over `bytes` bytes at p: loads past the end return 0.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_ptr(p)), (short)0,
+                                           (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+__device__ inline bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
+__device__ inline bf16x8 ld_bf16x8(const void* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+__device__ inline void st_bf16x8(void* p, bf16x8 v) {
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+
+// 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb.
+__device__ inline void ld_mod8(const wam_modulation& m, int D, int64_t row, int idx,
+                               int d, float out[8]) {
+  const int64_t b = row / m.tokens, t = row - b * m.tokens;
+  const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
+  const int64_t toff = (trow * 6 + idx) * (int64_t)D + d;
+  const int64_t tab = (int64_t)idx * D + d;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = ld_scalar(m.table, m.table_dtype, tab + e);
+  if (m.temb_dtype == WAM_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(m.temb) + toff);
+    float4 a = p[0], c = p[1];
+    out[0] += a.x; out[1] += a.y; out[2] += a.z; out[3] += a.w;
+    out[4] += c.x; out[5] += c.y; out[6] += c.z; out[7] += c.w;
+  } else {
+    bf16x8 v = ld_bf16x8(static_cast<const bf16*>(m.temb) + toff);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] += static_cast<float>(v[e]);
+  }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// GELU, tanh approximation: 0.5 x (1 + tanh(u)) = x * sigmoid(2u),
+// u = sqrt(2/pi) (x + 0.044715 x^3).  sigmoid via v_exp_f32 and v_rcp_f32.
+__device__ inline float gelu_tanh(float x) {
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(-2.0f * kLog2e * u);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+}  // namespace wam

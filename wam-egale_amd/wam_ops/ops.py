@@ -1,0 +1,260 @@
+"""Per-stage operators over torch tensors, each one C-ABI call into libwam_block.
+
+These are the building blocks of the native block (native.py) and the units
+the parity tests exercise one by one.  Tensors must be CUDA (HIP) tensors;
+shape/dtype contract violations raise RuntimeError before any launch, like
+the reference's TORCH_CHECKs (算子研究/wam_ops/optimized/csrc/block.cu:320-330).
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import (EPI_BIAS, EPI_BIAS_GATE_RES, EPI_BIAS_GELU, EPI_BIAS_RES, WAM_BF16,
+                   WAM_F32)
+
+__all__ = ["linear", "ln_modulate", "layer_norm_affine", "rms_rope", "attention",
+           "kv_layout", "kv_commit", "modulation", "stream_handle",
+           "EPI_BIAS", "EPI_BIAS_GELU", "EPI_BIAS_GATE_RES", "EPI_BIAS_RES"]
+
+
+def _req(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dtype_code(t):
+    if t.dtype == torch.float32:
+        return WAM_F32
+    if t.dtype == torch.bfloat16:
+        return WAM_BF16
+    raise RuntimeError(f"unsupported dtype {t.dtype} (need float32 or bfloat16)")
+
+
+def stream_handle(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dev(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _req(t.is_cuda, "native operators need GPU tensors")
+        if dev is None:
+            dev = t.device
+        _req(t.device == dev, "all tensors must be on one device")
+    return dev
+
+
+def _bf16(t, name):
+    _req(t.dtype == torch.bfloat16, f"{name} must be bfloat16 (got {t.dtype})")
+
+
+def modulation(table, temb, tokens):
+    """Describe mod = table[6, D] + temb[B, L, 6, D] for the C side.
+
+    table may be [1, 6, D] or [6, D] (model.py:738-739); temb is
+    [B, 1 or tokens, 6, D] (model.py:751-759)."""
+    _req(table.is_contiguous() and temb.is_contiguous(), "table/temb must be contiguous")
+    _req(temb.dim() == 4 and temb.shape[2] == 6, "temb must be [B, L, 6, D]")
+    _req(temb.shape[1] in (1, tokens), "temb length must be 1 or the token count")
+    _req(table.numel() == 6 * temb.shape[3], "scale_shift_table must hold 6 x D values")
+    m = _lib.Modulation()
+    m.table, m.table_dtype = table.data_ptr(), dtype_code(table)
+    m.temb, m.temb_dtype = temb.data_ptr(), dtype_code(temb)
+    m.temb_len, m.tokens = temb.shape[1], tokens
+    return m
+
+
+def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=None,
+           temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16):
+    """Y = epilogue(x W^T + b) on MFMA.  weights: one tensor or a list of up to 3
+    (one launch, outputs split per weight).  Returns a tensor or a list.
+    The residual may be bf16 or fp32; out_dtype=float32 is allowed for the
+    residual epilogues (the block keeps its residual stream in fp32)."""
+    single = torch.is_tensor(weights)
+    ws = [weights] if single else list(weights)
+    bs = [biases] if (single or biases is None) else list(biases)
+    if biases is None:
+        bs = [None] * len(ws)
+    _req(1 <= len(ws) <= 3 and len(bs) == len(ws), "1 to 3 weight segments")
+    dev = _dev(x, *ws, *[b for b in bs if b is not None], residual)
+    _bf16(x, "x")
+    _req(x.dim() >= 2 and x.stride(-1) == 1, "x must have a contiguous last dim")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    N = ws[0].shape[0]
+    for w, b in zip(ws, bs):
+        _bf16(w, "weight")
+        _req(w.is_contiguous() and w.shape == (N, K), f"weight must be [{N}, {K}] contiguous")
+        if b is not None:
+            _bf16(b, "bias")
+            _req(b.is_contiguous() and b.numel() == N, "bias must be [N]")
+    outs = out if out is not None else [torch.empty(*x.shape[:-1], N, dtype=out_dtype, device=dev)
+                                        for _ in ws]
+    if torch.is_tensor(outs):
+        outs = [outs]
+    a = _lib.LinearArgs()
+    a.a, a.lda, a.M, a.K = x2.data_ptr(), x2.stride(0), M, K
+    a.n_seg, a.seg_n, a.ldw = len(ws), N, K
+    for i, (w, b, o) in enumerate(zip(ws, bs, outs)):
+        _req(o.is_contiguous() and o.numel() == M * N and o.dtype == out_dtype, "out shape/dtype")
+        a.w[i] = w.data_ptr()
+        a.bias[i] = b.data_ptr() if b is not None else None
+        a.out[i] = o.data_ptr()
+    a.ldo = N
+    a.epilogue = epilogue
+    a.out_dtype = dtype_code(outs[0])
+    if epilogue in (EPI_BIAS_GATE_RES, EPI_BIAS_RES):
+        _req(residual is not None, "residual required")
+        r2 = residual.reshape(-1, N)
+        _req(r2.shape[0] == M and r2.stride(-1) == 1, "residual must be [M, N]")
+        a.res, a.ldr, a.res_dtype = r2.data_ptr(), r2.stride(0), dtype_code(r2)
+    if epilogue == EPI_BIAS_GATE_RES:
+        _req(table is not None and temb is not None and gate_index is not None, "gate needs table/temb")
+        a.gate = modulation(table, temb, tokens if tokens is not None else M)
+        a.gate_index = gate_index
+    _lib.check(_lib.lib().wam_linear(ctypes.byref(a), stream_handle(dev)), "wam_linear")
+    return outs[0] if single else outs
+
+
+def ln_modulate(x, table, temb, shift_index, eps=1e-6, out=None):
+    """bf16(LN(x) * (1 + mod[shift+1]) + mod[shift]), x [B, M, D] bf16 or fp32."""
+    dev = _dev(x, table, temb)
+    _req(x.dim() == 3 and x.is_contiguous(), "x must be [B, M, D] contiguous")
+    B, M, D = x.shape
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    a = _lib.LnArgs()
+    a.x, a.y, a.rows, a.D, a.eps, a.affine = x.data_ptr(), y.data_ptr(), B * M, D, eps, 0
+    a.x_dtype = dtype_code(x)
+    a.mod = modulation(table, temb, M)
+    a.shift_index = shift_index
+    _lib.check(_lib.lib().wam_ln_modulate(ctypes.byref(a), stream_handle(dev)), "wam_ln_modulate")
+    return y
+
+
+def layer_norm_affine(x, gamma, beta, eps=1e-6, out=None):
+    """bf16(LN(x) * gamma + beta) with fp32 statistics (norm2); x bf16 or fp32."""
+    dev = _dev(x, gamma, beta)
+    _req(x.is_contiguous(), "x must be contiguous")
+    D = x.shape[-1]
+    _req(gamma.numel() == D and beta.numel() == D and gamma.dtype == beta.dtype, "gamma/beta [D]")
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    a = _lib.LnArgs()
+    a.x, a.y, a.rows, a.D, a.eps, a.affine = x.data_ptr(), y.data_ptr(), x.numel() // D, D, eps, 1
+    a.x_dtype = dtype_code(x)
+    a.gamma, a.beta, a.gb_dtype = gamma.data_ptr(), beta.data_ptr(), dtype_code(gamma)
+    _lib.check(_lib.lib().wam_ln_modulate(ctypes.byref(a), stream_handle(dev)), "wam_ln_modulate")
+    return y
+
+
+def rms_rope(tensors, gammas, eps, freq=None, head_dim=128, out=None):
+    """RMSNorm across the full row (+ RoPE when freq is given) for 1-2 tensors
+    [B, M, D] bf16.  freq: complex64 [Bf, M, 1 or absent, head_dim/2]."""
+    ts = list(tensors)
+    gs = list(gammas)
+    es = list(eps) if isinstance(eps, (list, tuple)) else [eps] * len(ts)
+    dev = _dev(*ts, *gs, freq)
+    _req(1 <= len(ts) <= 2 and len(gs) == len(ts), "1 or 2 tensors")
+    B, M, D = ts[0].shape
+    outs = out if out is not None else [torch.empty_like(t) for t in ts]
+    a = _lib.RmsRopeArgs()
+    for i, (t, g, o) in enumerate(zip(ts, gs, outs)):
+        _bf16(t, "x")
+        _bf16(g, "gamma")
+        _req(t.shape == (B, M, D) and t.stride(-1) == 1 and t.stride(0) == M * t.stride(1),
+             "rms_rope tensors must be [B, M, D] with unit last stride")
+        _req(g.numel() == D, "gamma must be [D]")
+        a.x[i], a.y[i], a.gamma[i], a.eps[i] = t.data_ptr(), o.data_ptr(), g.data_ptr(), es[i]
+    _req(all(t.stride(1) == ts[0].stride(1) for t in ts), "equal row strides")
+    a.ldx, a.ldy = ts[0].stride(1), outs[0].stride(1)
+    a.n_tensors, a.rows, a.D, a.head_dim = len(ts), B * M, D, head_dim
+    if freq is not None:
+        _req(freq.dtype == torch.complex64 and freq.is_contiguous(), "freq must be contiguous complex64")
+        _req(freq.shape[1] == M and freq.shape[-1] == head_dim // 2, "freq must be [Bf, M, 1, hd/2]")
+        a.freq, a.freq_batch, a.tokens = freq.data_ptr(), freq.shape[0], M
+    _lib.check(_lib.lib().wam_rms_rope(ctypes.byref(a), stream_handle(dev)), "wam_rms_rope")
+    return outs
+
+
+def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, pool_rows=None,
+              kv_rows=None, scale=None, out=None):
+    """softmax(q [history || k]^T / sqrt(hd)) [history || v] per head.
+
+    q [B, Mq, H, 128]; k, v [Bk, Mk, H, 128] (any row stride, unit last dim);
+    history = pool_k/pool_v [Bp, P, H, 128] at slots[:n_hist] (int32, device),
+    pool row pool_rows[b] (int64) or b; own row kv_rows[b] or b."""
+    dev = _dev(q, k, v, pool_k, pool_v, slots, n_hist, pool_rows, kv_rows)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _bf16(t, n)
+        _req(t.dim() == 4 and t.shape[-1] == 128 and t.stride(-1) == 1 and t.stride(-2) == 128,
+             f"{n} must be [B, M, H, 128] with packed heads")
+    B, Mq, H, hd = q.shape
+    _req(k.shape == v.shape and k.shape[2] == H and k.stride() == v.stride(), "k/v shape")
+    o = out if out is not None else torch.empty(B, Mq, H, hd, dtype=torch.bfloat16, device=dev)
+    a = _lib.AttentionArgs()
+    a.q, a.q_bstride, a.q_rstride = q.data_ptr(), q.stride(0), q.stride(1)
+    a.o, a.o_bstride, a.o_rstride = o.data_ptr(), o.stride(0), o.stride(1)
+    a.B, a.Mq, a.H, a.head_dim = B, Mq, H, hd
+    if n_hist is not None:
+        _req(n_hist.dtype == torch.int32 and slots.dtype == torch.int32, "slots/n_hist are int32")
+        for t in (pool_k, pool_v):
+            _bf16(t, "pool")
+            _req(t.is_contiguous() and t.shape[2:] == (H, hd), "pool must be [Bp, P, H, 128]")
+        a.pool_k, a.pool_v = pool_k.data_ptr(), pool_v.data_ptr()
+        a.pool_bstride, a.pool_rstride = pool_k.stride(0), pool_k.stride(1)
+        a.pool_batch = pool_k.shape[0]
+        a.slots, a.n_hist_dev = slots.data_ptr(), n_hist.data_ptr()
+        if pool_rows is not None:
+            _req(pool_rows.dtype == torch.int64 and pool_rows.numel() == B, "pool_rows int64 [B]")
+            a.pool_rows = pool_rows.data_ptr()
+    a.k, a.v, a.kv_bstride, a.kv_rstride = k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1)
+    a.Mk, a.kv_batch = k.shape[1], k.shape[0]
+    if kv_rows is not None:
+        _req(kv_rows.dtype == torch.int64 and kv_rows.numel() == B, "kv_rows int64 [B]")
+        a.kv_rows = kv_rows.data_ptr()
+    a.scale = scale if scale is not None else 1.0 / math.sqrt(hd)
+    _lib.check(_lib.lib().wam_attention(ctypes.byref(a), stream_handle(dev)), "wam_attention")
+    return o
+
+
+def kv_layout(cache, tokens, update, candidate_rows=None):
+    """Pool bookkeeping of one self-attention call; mutates cache['mask'/'id'/'is_pred']
+    unless candidate_rows is given.  Returns (hist_slots, new_slots, info) int32."""
+    mask, ids, pred = cache["mask"], cache["id"], cache["is_pred"]
+    dev = _dev(mask, ids, pred, candidate_rows)
+    _req(mask.dtype == torch.bool and pred.dtype == torch.bool and ids.dtype == torch.int64,
+         "cache schema: mask/is_pred bool, id int64")
+    P = mask.numel()
+    hist = torch.empty(P, dtype=torch.int32, device=dev)
+    new = torch.empty(max(tokens, 1), dtype=torch.int32, device=dev)
+    info = torch.zeros(4, dtype=torch.int32, device=dev)
+    a = _lib.KvLayoutArgs()
+    a.mask, a.ids, a.is_pred, a.pool = mask.data_ptr(), ids.data_ptr(), pred.data_ptr(), P
+    a.tokens, a.update = tokens, update
+    a.candidate = 0 if candidate_rows is None else 1
+    if candidate_rows is not None:
+        a.rows, a.batch, a.pool_batch = candidate_rows.data_ptr(), candidate_rows.numel(), cache["k"].shape[0]
+    a.hist_slots, a.new_slots, a.info = hist.data_ptr(), new.data_ptr(), info.data_ptr()
+    _lib.check(_lib.lib().wam_kv_layout(ctypes.byref(a), stream_handle(dev)), "wam_kv_layout")
+    return hist, new, info
+
+
+def kv_commit(cache, k, v, new_slots):
+    """pool[b, new_slots[t]] = k[b, t] (and v), k/v [B, M, D] with unit last stride."""
+    dev = _dev(k, v, cache["k"], new_slots)
+    B, M = k.shape[:2]
+    D = cache["k"].shape[2] * cache["k"].shape[3]
+    a = _lib.KvCommitArgs()
+    a.k, a.v, a.ld = k.data_ptr(), v.data_ptr(), k.stride(1)
+    a.pool_k, a.pool_v = cache["k"].data_ptr(), cache["v"].data_ptr()
+    a.pool_bstride, a.pool_rstride = cache["k"].stride(0), cache["k"].stride(1)
+    a.new_slots, a.B, a.tokens, a.D = new_slots.data_ptr(), B, M, D
+    _lib.check(_lib.lib().wam_kv_commit(ctypes.byref(a), stream_handle(dev)), "wam_kv_commit")
