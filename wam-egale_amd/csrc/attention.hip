@@ -31,10 +31,13 @@ constexpr int kAttnKTile = 64;               // keys per LDS stage
 constexpr int kAttnKBytes = kAttnKTile * kAttnHD * 2;
 constexpr int kAttnStage = 2 * kAttnKBytes;  // K tile + V^T tile
 
-// K tile: [64 keys][128 d], 16 chunks of 16 B per row, chunk XOR key.
+// LDS bank layout: 64 banks x 4 bytes; ds_read_b128 serves 16 lanes per
+// cycle, and an MFMA operand fetch reads 16 consecutive rows at one chunk.
+// K tile: [64 keys][128 d], 256-byte rows (one bank line), chunk XOR key.
 __device__ inline int k_off(int key, int c) { return key * 256 + ((c ^ (key & 15)) << 4); }
-// V^T tile: [128 d][64 slots], 8 chunks per row, chunk XOR d.
-__device__ inline int vt_off(int d, int c) { return d * 128 + ((c ^ (d & 7)) << 4); }
+// V^T tile: [128 d][64 slots], 128-byte rows, two rows per bank line: chunk
+// XOR (d / 2) so that 16 consecutive rows hit 16 distinct 16-byte slots.
+__device__ inline int vt_off(int d, int c) { return d * 128 + ((c ^ ((d >> 1) & 7)) << 4); }
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(wam_attention_args a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * kAttnStage];

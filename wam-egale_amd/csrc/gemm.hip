@@ -13,13 +13,15 @@
 // (baseline/csrc/block.cu:119-129), the gated residual
 // x + y * gate (block.cu:90-102, gate 2 and 5) and the plain bf16 residual
 // add of cross attention (model.py:783).
+#include <stdlib.h>
+#include <string.h>
 #include "wam_common.h"
 
 namespace wam {
 
 struct LinearParams {
   const bf16* a; int64_t lda; int M, K;
-  int seg_n, n_tiles_per_seg, m_tiles, n_tiles;
+  int seg_n, n_tiles_per_seg, m_tiles, n_tiles, n_seg_count;
   const bf16* w[3]; int64_t ldw;
   const bf16* bias[3];
   void* out[3]; int64_t ldo;
@@ -28,30 +30,42 @@ struct LinearParams {
   wam_modulation gate; int gate_index;
 };
 
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_>
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0>
 struct GemmCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+  static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
+  static constexpr int SCHED = SCHED_;    // 1: pin DS-read / MFMA interleaving
   static constexpr int kWaves = WGM * WGN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
   static constexpr int TM = WTM / 32, TN = WTN / 32;
-  static constexpr int KCH = BK / 8;                 // 16-byte chunks per row
-  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  static constexpr int KCH = BK / 8;                     // 16-byte chunks per LDS row
+  static constexpr int ROW_BYTES = BK * 2;
+  static constexpr int A_BYTES = BM * ROW_BYTES, B_BYTES = BN * ROW_BYTES;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int ROWS_PER_PASS = kThreads / KCH;
-  static constexpr int A_LD = BM / ROWS_PER_PASS, B_LD = BN / ROWS_PER_PASS;
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "load split");
+  static constexpr int ROWS_PER_LOAD = 1024 / ROW_BYTES;  // one wave-wide 16 B/lane load
+  static constexpr int LOADS = (BM + BN) / ROWS_PER_LOAD;  // per stage, whole workgroup
+  static constexpr int LOADS_PER_WAVE = LOADS / kWaves;
+  static_assert(KCH == 8 || KCH == 4, "BK must be 64 or 32");
+  static_assert(LOADS % kWaves == 0 && BM % ROWS_PER_LOAD == 0, "load split");
+  static_assert((BM / ROWS_PER_LOAD) % kWaves == 0 && kWaves % 2 == 0, "loads per wave: A then W");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  static_assert(STAGES >= 2 && BLOCKS * STAGES * STAGE <= 160 * 1024, "LDS budget");
 };
 
-// Byte offset of 16-byte chunk `c` of LDS row `r`; the XOR spreads the 32
-// rows read by one MFMA operand fetch over distinct bank groups.
+// Byte offset of logical 16-byte chunk `c` of LDS row `r`.  The gfx950 LDS
+// has 64 banks of 4 bytes (256 bytes per cycle), and a ds_read_b128 serves 16
+// lanes per cycle.  An MFMA operand fetch reads 32 consecutive rows at one
+// logical chunk, so any 16 consecutive rows must land on 16 distinct 16-byte
+// bank slots: rows sharing a 256-byte bank line (2 rows of 128 bytes, 4 of 64)
+// are separated by the XOR of the row's index within its bank-line group.
 template <int KCH>
 __device__ inline int lds_off(int r, int c) {
-  return (r * KCH + (c ^ (r & (KCH - 1)))) * 16;
+  if constexpr (KCH == 8) return r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+  else return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
 }
 
-__device__ inline void ld_mod4(const wam_modulation& m, int D, int64_t row, int idx,
+__device__ inline void ld_mod4(const wam_modulation m, int D, int64_t row, int idx,
                                int d, float out[4]) {
   const int64_t b = row / m.tokens, t = row - b * m.tokens;
   const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
@@ -75,10 +89,55 @@ __device__ inline void ld_mod4(const wam_modulation& m, int D, int64_t row, int 
   }
 }
 
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Issue the direct-to-LDS loads of k-tile `kt` into LDS stage `stage`.  Load
+// g (0 <= g < LOADS) fills the 1 KB LDS block g, i.e. rows ROWS_PER_LOAD*g ..
+// +ROWS_PER_LOAD of the stacked [A rows; W rows] tile.  Wave w issues loads
+// g = w + i * kWaves; whether a load reads A or W depends on i only, so the
+// unrolled sequence has no branches.  a_lane / b_lane already include the
+// swizzle term of the wave's block parity (the wave count is even).
+template <class C>
+__device__ __forceinline__ void issue_stage(char* smem, __amdgpu_buffer_rsrc_t ra,
+                                            __amdgpu_buffer_rsrc_t rb, int wave, int a_lane,
+                                            int b_lane, int a_pitch, int b_pitch, int kt, int stage) {
+  char* base = smem + stage * C::STAGE;
+  const int ko = kt * C::BK * 2;
+  constexpr int A_ITERS = C::BM / C::ROWS_PER_LOAD / C::kWaves;
+#pragma unroll
+  for (int i = 0; i < C::LOADS_PER_WAVE; ++i) {
+    const int g = wave + i * C::kWaves;
+    char* dst = base + g * 1024;
+    if (i < A_ITERS)
+      buf_ld16_lds(ra, dst, a_lane + g * C::ROWS_PER_LOAD * a_pitch + ko);
+    else
+      buf_ld16_lds(rb, dst, b_lane + (g * C::ROWS_PER_LOAD - C::BM) * b_pitch + ko);
+  }
+}
+
+// MFMA operand fragments of one 16-deep k-step (logical chunk c of each row).
+template <class C>
+__device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase, int wm, int wn,
+                                            int l32, int c, bf16x8 (&fa)[C::TM], bf16x8 (&fb)[C::TN]) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+    fa[i] = ld_bf16x8(abase + lds_off<C::KCH>(wm * C::WTM + i * 32 + l32, c));
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j)
+    fb[j] = ld_bf16x8(bbase + lds_off<C::KCH>(wn * C::WTN + j * 32 + l32, c));
+}
+
 template <class C, int EPI>
-__global__ __launch_bounds__(C::kThreads, 1) void gemm_bf16_kernel(LinearParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(LinearParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[C::STAGES * C::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WGN, wn = wave % C::WGN;
 
   // Tile order: XCD-contiguous ranges, then groups of 8 m-tiles swept along n
@@ -95,39 +154,32 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_bf16_kernel(LinearParams 
   const int n0 = (tn - seg * p.n_tiles_per_seg) * C::BN;
   const int m0 = tm * C::BM;
 
-  const bf16* __restrict__ A = p.a;
+  const bf16* A = p.a;
   const bf16* wseg = seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]);
-  const bf16* __restrict__ W = wseg + (int64_t)n0 * p.ldw;
+  const bf16* W = wseg + (int64_t)n0 * p.ldw;
 
-  // Global -> register staging through buffer resources: thread owns chunk
-  // (tid % KCH) of rows tid / KCH + i * ROWS_PER_PASS.  Rows past M fall
-  // outside the A resource and load as zeros.
-  const int lc = tid % C::KCH, lr = tid / C::KCH;
+  // Direct-to-LDS staging.  Load g (0 <= g < LOADS) of a stage fills the
+  // 1 KB LDS block g, i.e. rows ROWS_PER_LOAD*g .. +ROWS_PER_LOAD of the
+  // stacked [A rows; W rows] tile; lane L lands at byte 16 L of that block,
+  // which is physical chunk L % KCH of row L / KCH, so it fetches the logical
+  // chunk that the swizzle maps there.  Rows of A past M fall outside the
+  // buffer resource and load as zeros.
   const uint32_t a_bytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u;
-  const __amdgpu_buffer_rsrc_t ra_src = make_rsrc(A + (int64_t)m0 * p.lda, a_bytes);
-  const __amdgpu_buffer_rsrc_t rb_src = make_rsrc(W, (uint32_t)((int64_t)C::BN * p.ldw * 2));
-  const int a_voff = (lr * (int)p.lda + lc * 8) * 2;
-  const int b_voff = (lr * (int)p.ldw + lc * 8) * 2;
-  const int a_step = C::ROWS_PER_PASS * (int)p.lda * 2;
-  const int b_step = C::ROWS_PER_PASS * (int)p.ldw * 2;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)m0 * p.lda, a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(W, (uint32_t)((int64_t)C::BN * p.ldw * 2));
+  const int lrow = lane / C::KCH, pchunk = lane % C::KCH;
+  // The swizzle term of row r = ROWS_PER_LOAD * g + lrow: for 128-byte rows
+  // (8 rows per block) it depends on the parity of g, for 64-byte rows (16
+  // rows per block) on lrow only.  With an even wave count every block a wave
+  // loads has the wave's parity.
+  const int r1 = C::ROWS_PER_LOAD + lrow;
+  const int chunk0 = C::KCH == 8 ? (pchunk ^ ((lrow >> 1) & 7)) : (pchunk ^ ((lrow >> 2) & 3));
+  const int chunk1 = C::KCH == 8 ? (pchunk ^ ((r1 >> 1) & 7)) : (pchunk ^ ((r1 >> 2) & 3));
+  const int lchunk = (wave & 1) ? chunk1 : chunk0;
+  const int a_lane = (lrow * (int)p.lda + lchunk * 8) * 2;
+  const int b_lane = (lrow * (int)p.ldw + lchunk * 8) * 2;
 
-  bf16x8 ra[C::A_LD], rb[C::B_LD];
-  auto gload = [&](int kt) {
-    const int ko = kt * C::BK * 2;
-#pragma unroll
-    for (int i = 0; i < C::A_LD; ++i) ra[i] = buf_ld16(ra_src, a_voff + i * a_step + ko);
-#pragma unroll
-    for (int i = 0; i < C::B_LD; ++i) rb[i] = buf_ld16(rb_src, b_voff + i * b_step + ko);
-  };
-  auto lstore = [&](int stage) {
-    char* base = smem + stage * C::STAGE;
-#pragma unroll
-    for (int i = 0; i < C::A_LD; ++i)
-      st_bf16x8(base + lds_off<C::KCH>(lr + i * C::ROWS_PER_PASS, lc), ra[i]);
-#pragma unroll
-    for (int i = 0; i < C::B_LD; ++i)
-      st_bf16x8(base + C::A_BYTES + lds_off<C::KCH>(lr + i * C::ROWS_PER_PASS, lc), rb[i]);
-  };
+  const int a_pitch = (int)p.lda * 2, b_pitch = (int)p.ldw * 2;
 
   f32x16 acc[C::TN][C::TM];
 #pragma unroll
@@ -136,34 +188,66 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_bf16_kernel(LinearParams 
     for (int i = 0; i < C::TM; ++i) acc[j][i] = f32x16{};
 
   const int nk = p.K / C::BK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
   const int half = lane >> 5, l32 = lane & 31;
+  constexpr int KSTEPS = C::BK / 16;
+  constexpr int MF = C::TM * C::TN, R = C::TM + C::TN;
+  static_assert(KSTEPS % 2 == 0, "fragment double buffer alternates per k-step");
+
+  // Prologue: all STAGES buffers in flight, wait for the first.
+#pragma unroll
+  for (int s = 0; s < C::STAGES; ++s)
+    if (s < nk) issue_stage<C>(smem, ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, s, s);
+  if (nk >= C::STAGES) wait_vmcnt<(C::STAGES - 1) * C::LOADS_PER_WAVE>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+
+  bf16x8 fa[2][C::TM], fb[2][C::TN];
+  fetch_frags<C>(smem, smem + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
+
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    const char* abase = smem + cur * C::STAGE;
+    const char* abase = smem + (kt % C::STAGES) * C::STAGE;
     const char* bbase = abase + C::A_BYTES;
+    // k-steps 0 .. KSTEPS-2: read the next step's fragments, then this
+    // step's MFMAs.
 #pragma unroll
-    for (int ks = 0; ks < C::BK / 16; ++ks) {
-      const int c = ks * 2 + half;
-      bf16x8 fa[C::TM], fb[C::TN];
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-        fa[i] = ld_bf16x8(abase + lds_off<C::KCH>(wm * C::WTM + i * 32 + l32, c));
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        fb[j] = ld_bf16x8(bbase + lds_off<C::KCH>(wn * C::WTN + j * 32 + l32, c));
+    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+      fetch_frags<C>(abase, bbase, wm, wn, l32, (ks + 1) * 2 + half, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
       for (int j = 0; j < C::TN; ++j)
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[j][i], 0, 0, 0);
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[j][i],
+                                                              0, 0, 0);
+      if constexpr (C::SCHED == 1) {
+#pragma unroll
+        for (int q = 0; q < (R < MF ? R : MF); ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        }
+        if constexpr (R < MF) __builtin_amdgcn_sched_group_barrier(0x008, MF - R, 0);
+        else if constexpr (R > MF) __builtin_amdgcn_sched_group_barrier(0x100, R - MF, 0);
+      }
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);
-    __syncthreads();
+    // Every LDS read of this stage is done (the last step's fragments are in
+    // registers), so the barrier goes here: the next stage's data is then
+    // visible, this stage's buffer can be refilled, and the next stage's
+    // first reads overlap this stage's last MFMAs.
+    if (kt + 1 < nk) {
+      if (kt + C::STAGES - 1 < nk) wait_vmcnt<(C::STAGES - 2) * C::LOADS_PER_WAVE>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (kt + C::STAGES < nk)
+        issue_stage<C>(smem, ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, kt + C::STAGES,
+                       kt % C::STAGES);
+      const char* na = smem + ((kt + 1) % C::STAGES) * C::STAGE;
+      fetch_frags<C>(na, na + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
+    }
+    constexpr int LAST = (KSTEPS - 1) & 1;
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[LAST][j], fa[LAST][i], acc[j][i], 0, 0, 0);
   }
 
   // Epilogue.  acc[j][i][4g + e] holds Y[m, n + e] with
@@ -225,13 +309,25 @@ __global__ __launch_bounds__(C::kThreads, 1) void gemm_bf16_kernel(LinearParams 
   }
 }
 
-using CfgBig = GemmCfg<256, 256, 64, 2, 2>;
-using CfgMid = GemmCfg<128, 128, 64, 2, 2>;
+// Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
+using Cfg256x256w4 = GemmCfg<256, 256, 64, 2, 2, 2>;
+using Cfg256x256w8 = GemmCfg<256, 256, 64, 2, 4, 2>;
+using Cfg256x256k32w4 = GemmCfg<256, 256, 32, 2, 2, 4>;
+using Cfg256x256k32w8 = GemmCfg<256, 256, 32, 2, 4, 4>;
+using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
+using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
+using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
+using Cfg256x128k32w4b2 = GemmCfg<256, 128, 32, 2, 2, 3, 2>;
+using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
+using Cfg128x256k32w4b2 = GemmCfg<128, 256, 32, 2, 2, 3, 2>;
 
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
+  WAM_REQUIRE(p.seg_n % C::BN == 0 && p.K % C::BK == 0,
+              "wam_linear: N=%d / K=%d do not fit a %dx%dx%d tile", p.seg_n, p.K, C::BM, C::BN, C::BK);
   p.n_tiles_per_seg = p.seg_n / C::BN;
   p.m_tiles = (p.M + C::BM - 1) / C::BM;
+  p.n_tiles = p.n_tiles_per_seg * p.n_seg_count;
   const int grid = p.m_tiles * p.n_tiles;
   switch (p.epi) {
     case WAM_EPI_BIAS:
@@ -248,6 +344,23 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
       break;
   }
   WAM_LAUNCHED("gemm_bf16_kernel");
+  return WAM_OK;
+}
+
+// Configuration by name (tuning override through WAM_GEMM_CFG), else by shape.
+static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool* found) {
+  *found = true;
+  if (!strcmp(name, "256x256w4")) return launch_gemm<Cfg256x256w4>(p, s);
+  if (!strcmp(name, "256x256w8")) return launch_gemm<Cfg256x256w8>(p, s);
+  if (!strcmp(name, "256x256k32w4")) return launch_gemm<Cfg256x256k32w4>(p, s);
+  if (!strcmp(name, "256x256k32w8")) return launch_gemm<Cfg256x256k32w8>(p, s);
+  if (!strcmp(name, "256x128w4")) return launch_gemm<Cfg256x128w4>(p, s);
+  if (!strcmp(name, "128x128w4")) return launch_gemm<Cfg128x128w4>(p, s);
+  if (!strcmp(name, "256x256w8s")) return launch_gemm<Cfg256x256w8s>(p, s);
+  if (!strcmp(name, "256x128k32w4b2")) return launch_gemm<Cfg256x128k32w4b2>(p, s);
+  if (!strcmp(name, "256x128k32w4b2s")) return launch_gemm<Cfg256x128k32w4b2s>(p, s);
+  if (!strcmp(name, "128x256k32w4b2")) return launch_gemm<Cfg128x256k32w4b2>(p, s);
+  *found = false;
   return WAM_OK;
 }
 
@@ -292,15 +405,20 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.res_f32 = a->res_dtype == WAM_F32;
   p.out_f32 = a->out_dtype == WAM_F32;
   p.gate = a->gate; p.gate_index = a->gate_index;
-  // Big tiles when the grid still covers the chip; otherwise 128x128.
-  const bool big = a->seg_n % 256 == 0 &&
-                   (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg >= 200;
-  if (big) {
-    p.n_tiles = a->n_seg * (a->seg_n / CfgBig::BN);
-    return launch_gemm<CfgBig>(p, s);
+  p.n_seg_count = a->n_seg;
+  const char* force = getenv("WAM_GEMM_CFG");
+  if (force && *force) {
+    bool found = false;
+    const int rc = launch_by_name(force, p, s, &found);
+    WAM_REQUIRE(found, "wam_linear: unknown WAM_GEMM_CFG '%s'", force);
+    return rc;
   }
-  p.n_tiles = a->n_seg * (a->seg_n / CfgMid::BN);
-  return launch_gemm<CfgMid>(p, s);
+  // Big tiles when the grid still covers the chip; otherwise smaller tiles.
+  const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
+  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_gemm<Cfg256x256w8s>(p, s);
+  const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
+  if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
+  return launch_gemm<Cfg128x128w4>(p, s);
 }
 
 }  // namespace wam

@@ -83,6 +83,12 @@ __device__ inline bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+// 16 bytes per lane from a buffer resource straight into LDS: lane L writes
+// bytes [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
+__device__ inline void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
 __device__ inline bf16x8 ld_bf16x8(const void* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
@@ -91,7 +97,7 @@ __device__ inline void st_bf16x8(void* p, bf16x8 v) {
 }
 
 // 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb.
-__device__ inline void ld_mod8(const wam_modulation& m, int D, int64_t row, int idx,
+__device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx,
                                int d, float out[8]) {
   const int64_t b = row / m.tokens, t = row - b * m.tokens;
   const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
