@@ -25,46 +25,60 @@
 namespace wam {
 
 constexpr int kAttnHD = 128;
-constexpr int kAttnWaves = 4;
-constexpr int kAttnQTile = 32 * kAttnWaves;  // queries per workgroup
-constexpr int kAttnKTile = 64;               // keys per LDS stage
-constexpr int kAttnKBytes = kAttnKTile * kAttnHD * 2;
-constexpr int kAttnStage = 2 * kAttnKBytes;  // K tile + V^T tile
+constexpr int kAttnKT = 64;                          // keys per LDS stage
+constexpr int kAttnTile = kAttnKT * kAttnHD * 2;     // 16 KB per K or V tile
+constexpr int kAttnStage = 2 * kAttnTile;            // K tile + V tile
+constexpr int kAttnStages = 3;
 
-// LDS bank layout: 64 banks x 4 bytes; ds_read_b128 serves 16 lanes per
-// cycle, and an MFMA operand fetch reads 16 consecutive rows at one chunk.
-// K tile: [64 keys][128 d], 256-byte rows (one bank line), chunk XOR key.
+// LDS layouts (64 banks x 4 bytes; 256-byte rows = one bank line).
+// K [64 keys][128 d]: an S^T operand fetch reads 16 consecutive keys at one
+// 16-byte chunk per cycle, so chunk XOR (key mod 16).
 __device__ inline int k_off(int key, int c) { return key * 256 + ((c ^ (key & 15)) << 4); }
-// V^T tile: [128 d][64 slots], 128-byte rows, two rows per bank line: chunk
-// XOR (d / 2) so that 16 consecutive rows hit 16 distinct 16-byte slots.
-__device__ inline int vt_off(int d, int c) { return d * 128 + ((c ^ ((d >> 1) & 7)) << 4); }
+// V [64 keys][128 d] in natural layout: a transposed read fetches 4
+// consecutive keys x 64 bytes per 32 lanes, so the 64-byte segment XOR
+// (key mod 4).
+__device__ inline int v_off(int key, int c) { return key * 256 + ((c ^ ((key & 3) << 2)) << 4); }
 
-__global__ __launch_bounds__(256, 2) void attention_kernel(wam_attention_args a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * kAttnStage];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n - 1 : r); }
+
+// Workgroup: W waves x 32 queries of one (batch row, head).  Wave w owns
+// queries q0 + 32 w .. +32 and keeps its Q fragments in registers.
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args a,
+                                                              const int* __restrict__ slots) {
+  // One __shared__ object per stage: the compiler tracks direct-to-LDS loads
+  // per object, so reading one stage while others are being filled does not
+  // wait for those loads.
+  __shared__ __attribute__((aligned(1024))) char lds0[kAttnStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kAttnStage];
+  __shared__ __attribute__((aligned(1024))) char lds2[kAttnStage];
+  static_assert(kAttnStages == 3, "three stage objects");
+#define WAM_ATTN_BUF(st) ((st) == 0 ? lds0 : (st) == 1 ? lds1 : lds2)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, half = lane >> 5;
+  constexpr int QT = 32 * W;
+  constexpr int LPW = 2 * kAttnTile / 1024 / W;  // 1 KB direct-to-LDS loads per wave per stage
+  static_assert(16 % W == 0, "waves must divide the 16 K blocks of a stage");
 
-  const int nqt = (a.Mq + kAttnQTile - 1) / kAttnQTile;
+  const int nqt = (a.Mq + QT - 1) / QT;
   const int id = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
   const int qt = id % nqt, bh = id / nqt;
   const int h = bh % a.H, b = bh / a.H;
 
   const int n_hist = a.n_hist_dev ? __builtin_amdgcn_readfirstlane(*a.n_hist_dev) : 0;
   const int n_tot = n_hist + a.Mk;
-  int prow = a.pool_rows ? (int)a.pool_rows[b] : b;
-  prow = prow < 0 ? 0 : (prow >= a.pool_batch ? a.pool_batch - 1 : prow);
-  int krow = a.kv_rows ? (int)a.kv_rows[b] : b;
-  krow = krow < 0 ? 0 : (krow >= a.kv_batch ? a.kv_batch - 1 : krow);
-  prow = __builtin_amdgcn_readfirstlane(prow);
-  krow = __builtin_amdgcn_readfirstlane(krow);
-
+  const int prow = __builtin_amdgcn_readfirstlane(a.pool_rows ? clamp_row((int)a.pool_rows[b], a.pool_batch)
+                                                              : (a.pool_batch > 0 ? clamp_row(b, a.pool_batch) : 0));
+  const int krow = __builtin_amdgcn_readfirstlane(a.kv_rows ? clamp_row((int)a.kv_rows[b], a.kv_batch)
+                                                            : clamp_row(b, a.kv_batch));
   const bf16* pool_k = a.pool_k ? static_cast<const bf16*>(a.pool_k) + (int64_t)prow * a.pool_bstride + h * kAttnHD : nullptr;
   const bf16* pool_v = a.pool_v ? static_cast<const bf16*>(a.pool_v) + (int64_t)prow * a.pool_bstride + h * kAttnHD : nullptr;
   const bf16* own_k = static_cast<const bf16*>(a.k) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
   const bf16* own_v = static_cast<const bf16*>(a.v) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
 
-  // Q fragments (B operand of S^T): query qi, d = ks*16 + half*8 .. +8.
-  const int qi = qt * kAttnQTile + wave * 32 + l32;
+  // Q fragments (B operand of S^T = K Q^T): query qi, d = 16 ks + 8 half .. +8.
+  const int qi = qt * QT + wave * 32 + l32;
   const bool q_ok = qi < a.Mq;
   const bf16* qp = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride +
                    (int64_t)(q_ok ? qi : 0) * a.q_rstride + h * kAttnHD + half * 8;
@@ -75,115 +89,145 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(wam_attention_args a)
     if (!q_ok) qf[ks] = bf16x8{};
   }
 
-  auto key_row = [&](const bf16* pool, const bf16* own, int j) -> const bf16* {
-    j = j < n_tot ? j : n_tot - 1;
-    return j < n_hist ? pool + (int64_t)a.slots[j] * a.pool_rstride
-                      : own + (int64_t)(j - n_hist) * a.kv_rstride;
-  };
-
-  // Staging: K thread -> chunk (tid & 15) of keys (tid >> 4) + 16 i;
-  //          V thread -> d-octet (tid >> 4) of keys 4 (tid & 15) + i.
-  const int kc = tid & 15, kr = tid >> 4;
-  const int vq = tid & 15, vd = tid >> 4;
-  bf16x8 rk[4], rv[4];
-  auto gload = [&](int t) {
-    const int j0 = t * kAttnKTile;
+  // Direct-to-LDS staging.  Load g (0..31) of a stage fills 1 KB block g:
+  // blocks 0-15 are the K tile, 16-31 the V tile, 4 rows (keys) each; lane L
+  // lands in row 4 (g % 16) + L / 16, physical chunk L % 16, and fetches the
+  // logical chunk the swizzle maps there.  Load i of wave w is g = w + i W.
+  const int lrow = lane >> 4, pch = lane & 15;
+  auto issue = [=](int t, char* base) {
+    const int j0 = t * kAttnKT;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rk[i] = ld_bf16x8(key_row(pool_k, own_k, j0 + kr + 16 * i) + kc * 8);
+    for (int i = 0; i < LPW; ++i) {
+      const int g = wave + i * W;
+      const bool is_k = i < 16 / W;                 // compile-time per i
+      const int gb = g & 15;
+      const int row = 4 * gb + lrow;
+      // slot indices of the block's 4 rows: wave-uniform loads
+      const int jj = j0 + 4 * gb;
+      int sl[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rv[i] = ld_bf16x8(key_row(pool_v, own_v, j0 + 4 * vq + i) + vd * 8);
-  };
-  // V^T slot of the key quad 4*vq..4*vq+3: 16-key group g = vq/4, and inside
-  // the group quads 0,1,2,3 go to slots 0-3, 8-11, 4-7, 12-15.
-  const int vgrp = vq >> 2, vqq = vq & 3;
-  const int vchunk = 2 * vgrp + (vqq & 1), vbyte = (vqq >> 1) * 8;
-  auto lstore = [&](int stage) {
-    char* kb = smem + stage * kAttnStage;
-    char* vb = kb + kAttnKBytes;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st_bf16x8(kb + k_off(kr + 16 * i, kc), rk[i]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = vd * 8 + e;
-      bf16x4 t;
-      t[0] = rv[0][e]; t[1] = rv[1][e]; t[2] = rv[2][e]; t[3] = rv[3][e];
-      *reinterpret_cast<bf16x4*>(vb + vt_off(d, vchunk) + vbyte) = t;
+      for (int r = 0; r < 4; ++r) {
+        const int j = __builtin_amdgcn_readfirstlane(min(jj + r, n_tot - 1));
+        sl[r] = j < n_hist ? slots[j] : 0;
+      }
+      const int slot = lrow == 0 ? sl[0] : (lrow == 1 ? sl[1] : (lrow == 2 ? sl[2] : sl[3]));
+      const int j = min(jj + lrow, n_tot - 1);
+      const int c = is_k ? (pch ^ (row & 15)) : (pch ^ ((row & 3) << 2));
+      const bf16* src = j < n_hist ? (is_k ? pool_k : pool_v) + (int64_t)slot * a.pool_rstride
+                                   : (is_k ? own_k : own_v) + (int64_t)(j - n_hist) * a.kv_rstride;
+      g_ld16_lds(src + c * 8, base + (is_k ? 0 : kAttnTile) + gb * 1024);
     }
   };
 
-  const float c = a.scale * kLog2e;
+  const float sc = a.scale * kLog2e;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
 
-  const int ntiles = (n_tot + kAttnKTile - 1) / kAttnKTile;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-    const char* kb = smem + cur * kAttnStage;
-    const char* vb = kb + kAttnKBytes;
+  // Transposed-read source addresses of this lane inside a V tile, per
+  // (dt, ks, part): keys 16 ks + 4 half + 8 part + (lane % 16) / 4,
+  // d = 32 dt + 16 ((lane / 16) % 2) + 4 (lane % 4).
+  const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
 
-    f32x16 s[2];
+  const int ntiles = (n_tot + kAttnKT - 1) / kAttnKT;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      s[kt] = f32x16{};
-      const int key = kt * 32 + l32;
+  for (int st = 0; st < kAttnStages - 1; ++st)
+    if (st < ntiles) issue(st, WAM_ATTN_BUF(st));
+
+  // The tile loop is unrolled by the stage count so that every LDS reference
+  // is to a fixed __shared__ object.
+  for (int t0 = 0; t0 < ntiles; t0 += kAttnStages) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(key, 2 * ks + half)),
-                                                        qf[ks], s[kt], 0, 0, 0);
-    }
-    if ((t + 1) * kAttnKTile > n_tot) {
+    for (int st = 0; st < kAttnStages; ++st) {
+      const int t = t0 + st;
+      if (t >= ntiles) break;
+      if (t + kAttnStages - 2 < ntiles) {
+        // stages t+1 .. t+STAGES-2 may still be in flight
+        __builtin_amdgcn_s_waitcnt((((kAttnStages - 2) * LPW) & 15) | ((((kAttnStages - 2) * LPW) >> 4) << 14) |
+                                   (7 << 4) | (15 << 8));
+      } else {
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      }
+      __builtin_amdgcn_s_barrier();
+      if (t + kAttnStages - 1 < ntiles) issue(t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages));
+      const char* kb = WAM_ATTN_BUF(st);
+      const char* vb = kb + kAttnTile;
+
+      f32x16 s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = f32x16{};
+        const int key = kt * 32 + l32;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(key, 2 * ks + half)), qf[ks],
+                                                          s[kt], 0, 0, 0);
+      }
+      if ((t + 1) * kAttnKT > n_tot) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int j = t * kAttnKT + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (j >= n_tot) s[kt][v] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Lazy rescaling: the running max m_run only moves when this tile's max
+      // exceeds it by more than 2^8 (log2 units), so exp2(s - m_run) <= 2^8;
+      // the O/l rescale runs only when some lane's max moved.  The result
+      // sum(p v) / sum(p) does not depend on which max is used.
+      const float mt = mx * sc;
+      const bool grow = mt > m_run + 8.0f;
+      const float m_new = grow ? mt : m_run;
+      float psum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int j = t * kAttnKTile + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (j >= n_tot) s[kt][v] = -INFINITY;
+          const float pv = __builtin_amdgcn_exp2f(s[kt][v] * sc - m_new);
+          s[kt][v] = pv;
+          psum += pv;
         }
-    }
-    float mx = -INFINITY;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx * c);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float pv = __builtin_amdgcn_exp2f(s[kt][v] * c - m_new);
-        s[kt][v] = pv;
-        psum += pv;
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      l_run += psum;
+      m_run = m_new;
 
-    bf16x8 pb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int u = 0; u < 8; ++u) pb[ks][u] = static_cast<bf16>(s[ks >> 1][(ks & 1) * 8 + u]);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      const int d = dt * 32 + l32;
+      bf16x8 pb[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(vb + vt_off(d, 2 * ks + half)),
-                                                        pb[ks], o[dt], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) pb[ks][u] = static_cast<bf16>(s[ks >> 1][(ks & 1) * 8 + u]);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          bf16x8 va;
+#pragma unroll
+          for (int part = 0; part < 2; ++part) {
+            const int key = 16 * ks + 4 * half + 8 * part + (tr_i >> 2);
+            const int d = 32 * dt + 16 * tr_gh + 4 * (tr_i & 3);
+            const bf16x4 t4 = ld_tr16(vb + v_off(key, d >> 3) + (d & 7) * 2);
+            va[4 * part + 0] = t4[0]; va[4 * part + 1] = t4[1];
+            va[4 * part + 2] = t4[2]; va[4 * part + 3] = t4[3];
+          }
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[ks], o[dt], 0, 0, 0);
+        }
+      }
     }
-    if (t + 1 < ntiles) lstore(cur ^ 1);
-    __syncthreads();
   }
+#undef WAM_ATTN_BUF
 
   const float l = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.f / l;
@@ -193,10 +237,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(wam_attention_args a)
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        bf16x4 t;
+        bf16x4 t4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] = static_cast<bf16>(o[dt][4 * g + e] * inv);
-        *reinterpret_cast<bf16x4*>(op + dt * 32 + 8 * g + 4 * half) = t;
+        for (int e = 0; e < 4; ++e) t4[e] = static_cast<bf16>(o[dt][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4*>(op + dt * 32 + 8 * g + 4 * half) = t4;
       }
   }
 }
@@ -225,10 +269,15 @@ int attention(const wam_attention_args* a, hipStream_t s) {
     WAM_REQUIRE(a->B <= a->kv_batch || a->kv_batch == 1,
                 "wam_attention: B=%d exceeds kv batch %d", a->B, a->kv_batch);
   if (a->Mq == 0) return WAM_OK;
-  const int nqt = (a->Mq + kAttnQTile - 1) / kAttnQTile;
-  const int64_t grid = (int64_t)nqt * a->H * a->B;
-  WAM_REQUIRE(grid < (1 << 30), "wam_attention: grid too large");
-  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)grid), dim3(256), 0, s, *a);
+  // 8 waves (256 queries) per workgroup when that still fills the chip.
+  const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
+  if (grid8 >= 256) {
+    WAM_REQUIRE(grid8 < (1 << 30), "wam_attention: grid too large");
+    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots);
+  } else {
+    const int64_t grid4 = (int64_t)((a->Mq + 127) / 128) * a->H * a->B;
+    hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid4), dim3(256), 0, s, *a, a->slots);
+  }
   WAM_LAUNCHED("attention_kernel");
   return WAM_OK;
 }

@@ -104,10 +104,9 @@ __device__ inline void wait_vmcnt() {
 // unrolled sequence has no branches.  a_lane / b_lane already include the
 // swizzle term of the wave's block parity (the wave count is even).
 template <class C>
-__device__ __forceinline__ void issue_stage(char* smem, __amdgpu_buffer_rsrc_t ra,
+__device__ __forceinline__ void issue_stage(char* base, __amdgpu_buffer_rsrc_t ra,
                                             __amdgpu_buffer_rsrc_t rb, int wave, int a_lane,
-                                            int b_lane, int a_pitch, int b_pitch, int kt, int stage) {
-  char* base = smem + stage * C::STAGE;
+                                            int b_lane, int a_pitch, int b_pitch, int kt) {
   const int ko = kt * C::BK * 2;
   constexpr int A_ITERS = C::BM / C::ROWS_PER_LOAD / C::kWaves;
 #pragma unroll
@@ -135,7 +134,14 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
 
 template <class C, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(LinearParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[C::STAGES * C::STAGE];
+  // One __shared__ object per pipeline stage: the compiler tracks the
+  // direct-to-LDS loads per object, so reading one stage while another is
+  // being filled needs no wait on the outstanding loads.
+  __shared__ __attribute__((aligned(1024))) char lds0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds2[C::STAGES > 2 ? C::STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) char lds3[C::STAGES > 3 ? C::STAGE : 16];
+#define WAM_GEMM_BUF(st) ((st) == 0 ? lds0 : (st) == 1 ? lds1 : (st) == 2 ? lds2 : lds3)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WGN, wn = wave % C::WGN;
@@ -195,60 +201,67 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 
   // Prologue: all STAGES buffers in flight, wait for the first.
 #pragma unroll
-  for (int s = 0; s < C::STAGES; ++s)
-    if (s < nk) issue_stage<C>(smem, ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, s, s);
+  for (int st = 0; st < C::STAGES; ++st)
+    if (st < nk) issue_stage<C>(WAM_GEMM_BUF(st), ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, st);
   if (nk >= C::STAGES) wait_vmcnt<(C::STAGES - 1) * C::LOADS_PER_WAVE>();
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
 
   bf16x8 fa[2][C::TM], fb[2][C::TN];
-  fetch_frags<C>(smem, smem + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
+  fetch_frags<C>(lds0, lds0 + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const char* abase = smem + (kt % C::STAGES) * C::STAGE;
-    const char* bbase = abase + C::A_BYTES;
-    // k-steps 0 .. KSTEPS-2: read the next step's fragments, then this
-    // step's MFMAs.
+  // The k loop is unrolled by STAGES so that every buffer reference is to a
+  // fixed __shared__ object.
+  for (int kt0 = 0; kt0 < nk; kt0 += C::STAGES) {
 #pragma unroll
-    for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
-      fetch_frags<C>(abase, bbase, wm, wn, l32, (ks + 1) * 2 + half, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+    for (int st = 0; st < C::STAGES; ++st) {
+      const int kt = kt0 + st;
+      if (kt >= nk) break;
+      const char* abase = WAM_GEMM_BUF(st);
+      const char* bbase = abase + C::A_BYTES;
+      // k-steps 0 .. KSTEPS-2: read the next step's fragments, then this
+      // step's MFMAs.
+#pragma unroll
+      for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+        fetch_frags<C>(abase, bbase, wm, wn, l32, (ks + 1) * 2 + half, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int i = 0; i < C::TM; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[j][i],
+                                                                0, 0, 0);
+        if constexpr (C::SCHED == 1) {
+#pragma unroll
+          for (int q = 0; q < (R < MF ? R : MF); ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          }
+          if constexpr (R < MF) __builtin_amdgcn_sched_group_barrier(0x008, MF - R, 0);
+          else if constexpr (R > MF) __builtin_amdgcn_sched_group_barrier(0x100, R - MF, 0);
+        }
+      }
+      // Every LDS read of this stage is done (the last step's fragments are
+      // in registers), so the barrier goes here: the next stage's data is
+      // then visible, this stage's buffer can be refilled, and the next
+      // stage's first reads overlap this stage's last MFMAs.
+      if (kt + 1 < nk) {
+        if (kt + C::STAGES - 1 < nk) wait_vmcnt<(C::STAGES - 2) * C::LOADS_PER_WAVE>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + C::STAGES < nk)
+          issue_stage<C>(WAM_GEMM_BUF(st), ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, kt + C::STAGES);
+        const char* na = WAM_GEMM_BUF((st + 1) % C::STAGES);
+        fetch_frags<C>(na, na + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
+      }
+      constexpr int LAST = (KSTEPS - 1) & 1;
 #pragma unroll
       for (int j = 0; j < C::TN; ++j)
 #pragma unroll
         for (int i = 0; i < C::TM; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[j][i],
-                                                              0, 0, 0);
-      if constexpr (C::SCHED == 1) {
-#pragma unroll
-        for (int q = 0; q < (R < MF ? R : MF); ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        }
-        if constexpr (R < MF) __builtin_amdgcn_sched_group_barrier(0x008, MF - R, 0);
-        else if constexpr (R > MF) __builtin_amdgcn_sched_group_barrier(0x100, R - MF, 0);
-      }
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[LAST][j], fa[LAST][i], acc[j][i], 0, 0, 0);
     }
-    // Every LDS read of this stage is done (the last step's fragments are in
-    // registers), so the barrier goes here: the next stage's data is then
-    // visible, this stage's buffer can be refilled, and the next stage's
-    // first reads overlap this stage's last MFMAs.
-    if (kt + 1 < nk) {
-      if (kt + C::STAGES - 1 < nk) wait_vmcnt<(C::STAGES - 2) * C::LOADS_PER_WAVE>();
-      else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-      if (kt + C::STAGES < nk)
-        issue_stage<C>(smem, ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, kt + C::STAGES,
-                       kt % C::STAGES);
-      const char* na = smem + ((kt + 1) % C::STAGES) * C::STAGE;
-      fetch_frags<C>(na, na + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
-    }
-    constexpr int LAST = (KSTEPS - 1) & 1;
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[LAST][j], fa[LAST][i], acc[j][i], 0, 0, 0);
   }
+#undef WAM_GEMM_BUF
 
   // Epilogue.  acc[j][i][4g + e] holds Y[m, n + e] with
   //   m = m0 + wm*WTM + i*32 + l32,  n = n0 + wn*WTN + j*32 + 8g + 4*half.

@@ -17,70 +17,104 @@
 namespace wam {
 
 // ------------------------------------------------------------- LayerNorm
-template <int CH>  // 16-byte chunks per lane (D <= CH * 512)
-__global__ __launch_bounds__(256) void ln_modulate_kernel(wam_ln_args a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
-  const int D = a.D, nch = D >> 3;
-  float v[CH][8];
-  float s = 0.f;
+// Each wave normalises kRowsPerWave consecutive rows, loading row r+1 while
+// it reduces row r; the modulation (or affine) vectors are loaded once and
+// reused while consecutive rows share a sample.
+constexpr int kRowsPerWave = 1;
+
+template <int CH, bool XF32>
+__device__ inline void ln_load_row(const void* x, int64_t row, int D, int lane, float v[CH][8]) {
+  const int nch = D >> 3;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = lane + c * 64;
     if (ch < nch) {
-      if (a.x_dtype == WAM_F32) {
-        const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + row * D + ch * 8);
-        const float4 p0 = xp[0], p1 = xp[1];
-        v[c][0] = p0.x; v[c][1] = p0.y; v[c][2] = p0.z; v[c][3] = p0.w;
-        v[c][4] = p1.x; v[c][5] = p1.y; v[c][6] = p1.z; v[c][7] = p1.w;
-      } else {
-        const bf16x8 t = ld_bf16x8(static_cast<const bf16*>(a.x) + row * D + ch * 8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = static_cast<float>(t[e]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[c][e];
+      ld8_f32(x, XF32 ? WAM_F32 : WAM_BF16, row * D + ch * 8, v[c]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[c][e] = 0.f;
     }
   }
-  const float mean = wave_sum(s) / D;
-  float q = 0.f;
+}
+
+template <int CH, bool XF32>
+__global__ __launch_bounds__(256) void ln_modulate_kernel(wam_ln_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  if (row0 >= a.rows) return;
+  const int D = a.D, nch = D >> 3;
+  float mul[CH][8], add[CH][8];
+  int64_t mod_key = -1;  // sample (or token row) whose modulation is loaded
+  float v[CH][8], nxt[CH][8];
+  ln_load_row<CH, XF32>(a.x, row0, D, lane, v);
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int ch = lane + c * 64;
-    if (ch < nch) {
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const int64_t row = row0 + r;
+    if (row >= a.rows) break;
+    if (r + 1 < kRowsPerWave && row + 1 < a.rows) ln_load_row<CH, XF32>(a.x, row + 1, D, lane, nxt);
+    const int64_t key = a.affine ? 0
+                      : (a.mod.temb_len == 1 ? row / a.mod.tokens : row);
+    if (key != mod_key) {
+      mod_key = key;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) { const float d = v[c][e] - mean; q += d * d; }
-    }
-  }
-  const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
-  bf16* y = static_cast<bf16*>(a.y) + row * D;
+      for (int c = 0; c < CH; ++c) {
+        const int ch = lane + c * 64;
+        if (ch >= nch) continue;
+        if (a.affine) {
+          ld8_f32(a.gamma, a.gb_dtype, ch * 8, mul[c]);
+          ld8_f32(a.beta, a.gb_dtype, ch * 8, add[c]);
+        } else {
+          ld_mod8(a.mod, D, row, a.shift_index, ch * 8, add[c]);
+          ld_mod8(a.mod, D, row, a.shift_index + 1, ch * 8, mul[c]);
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int ch = lane + c * 64;
-    if (ch >= nch) continue;
-    const int d0 = ch * 8;
-    float mul[8], add[8];
-    if (a.affine) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        mul[e] = ld_scalar(a.gamma, a.gb_dtype, d0 + e);
-        add[e] = ld_scalar(a.beta, a.gb_dtype, d0 + e);
+          for (int e = 0; e < 8; ++e) mul[c][e] += 1.f;
+        }
       }
-    } else {
-      ld_mod8(a.mod, D, row, a.shift_index, d0, add);
-      ld_mod8(a.mod, D, row, a.shift_index + 1, d0, mul);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mul[e] += 1.f;
     }
-    bf16x8 o;
+    float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[e] + add[e]);
-    st_bf16x8(y + d0, o);
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[c][e];
+    const float mean = wave_sum(s) / D;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (lane + c * 64 < nch) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = v[c][e] - mean; q += d * d; }
+      }
+    }
+    const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
+    bf16* y = static_cast<bf16*>(a.y) + row * D;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = lane + c * 64;
+      if (ch >= nch) continue;
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[c][e] + add[c][e]);
+      st_bf16x8(y + ch * 8, o);
+    }
+    if (r + 1 < kRowsPerWave) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = nxt[c][e];
+    }
   }
+}
+
+template <bool XF32>
+static void launch_ln(const wam_ln_args* a, hipStream_t s) {
+  const int64_t waves = (a->rows + kRowsPerWave - 1) / kRowsPerWave;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  const int ch = (a->D / 8 + 63) / 64;
+  if (ch <= 1) hipLaunchKernelGGL((ln_modulate_kernel<1, XF32>), grid, block, 0, s, *a);
+  else if (ch <= 2) hipLaunchKernelGGL((ln_modulate_kernel<2, XF32>), grid, block, 0, s, *a);
+  else if (ch <= 3) hipLaunchKernelGGL((ln_modulate_kernel<3, XF32>), grid, block, 0, s, *a);
+  else if (ch <= 6) hipLaunchKernelGGL((ln_modulate_kernel<6, XF32>), grid, block, 0, s, *a);
+  else hipLaunchKernelGGL((ln_modulate_kernel<8, XF32>), grid, block, 0, s, *a);
 }
 
 int ln_modulate(const wam_ln_args* a, hipStream_t s) {
@@ -98,13 +132,8 @@ int ln_modulate(const wam_ln_args* a, hipStream_t s) {
                 "wam_ln_modulate: modulation contract (shift index %d)", a->shift_index);
   }
   if (a->rows == 0) return WAM_OK;
-  const dim3 grid((a->rows + 3) / 4), block(256);
-  const int ch = (a->D / 8 + 63) / 64;
-  if (ch <= 1) hipLaunchKernelGGL(ln_modulate_kernel<1>, grid, block, 0, s, *a);
-  else if (ch <= 2) hipLaunchKernelGGL(ln_modulate_kernel<2>, grid, block, 0, s, *a);
-  else if (ch <= 3) hipLaunchKernelGGL(ln_modulate_kernel<3>, grid, block, 0, s, *a);
-  else if (ch <= 6) hipLaunchKernelGGL(ln_modulate_kernel<6>, grid, block, 0, s, *a);
-  else hipLaunchKernelGGL(ln_modulate_kernel<8>, grid, block, 0, s, *a);
+  if (a->x_dtype == WAM_F32) launch_ln<true>(a, s);
+  else launch_ln<false>(a, s);
   WAM_LAUNCHED("ln_modulate_kernel");
   return WAM_OK;
 }

@@ -89,6 +89,22 @@ __device__ inline void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 }
 
+// 16 bytes per lane from a global address straight into LDS: lane L writes
+// bytes [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
+__device__ inline void g_ld16_lds(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, source lane j addresses 4
+// consecutive 16-bit elements; lane i receives element (i % 4) of source
+// lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12 (a 4 x 16 transpose).
+__device__ inline bf16x4 ld_tr16(const void* lds) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)lds);
+  return __builtin_bit_cast(bf16x4, v);
+}
+
 __device__ inline bf16x8 ld_bf16x8(const void* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
@@ -96,31 +112,47 @@ __device__ inline void st_bf16x8(void* p, bf16x8 v) {
   *reinterpret_cast<bf16x8*>(p) = v;
 }
 
-// 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb.
-__device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx,
-                               int d, float out[8]) {
-  const int64_t b = row / m.tokens, t = row - b * m.tokens;
-  const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
-  const int64_t toff = (trow * 6 + idx) * (int64_t)D + d;
-  const int64_t tab = (int64_t)idx * D + d;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = ld_scalar(m.table, m.table_dtype, tab + e);
-  if (m.temb_dtype == WAM_F32) {
-    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(m.temb) + toff);
-    float4 a = p[0], c = p[1];
-    out[0] += a.x; out[1] += a.y; out[2] += a.z; out[3] += a.w;
-    out[4] += c.x; out[5] += c.y; out[6] += c.z; out[7] += c.w;
+// 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb,
+// for token row `row` (b = row / tokens, t = row % tokens).
+__device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[8]) {
+  if (dtype == WAM_F32) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + off);
+    const float4 a = q[0], c = q[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
   } else {
-    bf16x8 v = ld_bf16x8(static_cast<const bf16*>(m.temb) + toff);
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(p) + off);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] += static_cast<float>(v[e]);
+    for (int e = 0; e < 8; ++e) out[e] = static_cast<float>(v[e]);
   }
 }
-
-__device__ inline float wave_sum(float v) {
+__device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx, int d, float out[8]) {
+  const int64_t b = row / m.tokens, t = row - b * m.tokens;
+  const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
+  float tb[8];
+  ld8_f32(m.table, m.table_dtype, (int64_t)idx * D + d, out);
+  ld8_f32(m.temb, m.temb_dtype, (trow * 6 + idx) * (int64_t)D + d, tb);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  for (int e = 0; e < 8; ++e) out[e] += tb[e];
+}
+
+// Sum over the 64 lanes of a wave: DPP adds within each 16-lane row
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+// then the four row sums through readlane.  The result is wave-uniform.
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ inline float wave_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  const int i = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
 }
 
 // GELU, tanh approximation: 0.5 x (1 + tanh(u)) = x * sigmoid(2u),
