@@ -34,7 +34,8 @@ template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
-  static constexpr int SCHED = SCHED_;    // 1: pin DS-read / MFMA interleaving
+  static constexpr int SCHED = SCHED_;    // 1: alternate DS reads and MFMAs; 2: all reads of
+                                          // the next k-step, then this step's MFMAs
   static constexpr int kWaves = WGM * WGN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -50,7 +51,7 @@ struct GemmCfg {
   static_assert(LOADS % kWaves == 0 && BM % ROWS_PER_LOAD == 0, "load split");
   static_assert((BM / ROWS_PER_LOAD) % kWaves == 0 && kWaves % 2 == 0, "loads per wave: A then W");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
-  static_assert(STAGES >= 2 && BLOCKS * STAGES * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(STAGES >= 2 && BLOCKS * (STAGES * STAGE + (5 - STAGES) * 1024) <= 160 * 1024, "LDS budget");
 };
 
 // Byte offset of logical 16-byte chunk `c` of LDS row `r`.  The gfx950 LDS
@@ -104,8 +105,7 @@ __device__ inline void wait_vmcnt() {
 // unrolled sequence has no branches.  a_lane / b_lane already include the
 // swizzle term of the wave's block parity (the wave count is even).
 template <class C>
-__device__ __forceinline__ void issue_stage(char* base, __amdgpu_buffer_rsrc_t ra,
-                                            __amdgpu_buffer_rsrc_t rb, int wave, int a_lane,
+__device__ __forceinline__ void issue_stage(char* base, i32x4 ra, i32x4 rb, int wave, int a_lane,
                                             int b_lane, int a_pitch, int b_pitch, int kt) {
   const int ko = kt * C::BK * 2;
   constexpr int A_ITERS = C::BM / C::ROWS_PER_LOAD / C::kWaves;
@@ -114,9 +114,9 @@ __device__ __forceinline__ void issue_stage(char* base, __amdgpu_buffer_rsrc_t r
     const int g = wave + i * C::kWaves;
     char* dst = base + g * 1024;
     if (i < A_ITERS)
-      buf_ld16_lds(ra, dst, a_lane + g * C::ROWS_PER_LOAD * a_pitch + ko);
+      asm_ld16_lds(ra, dst, a_lane + g * C::ROWS_PER_LOAD * a_pitch + ko);
     else
-      buf_ld16_lds(rb, dst, b_lane + (g * C::ROWS_PER_LOAD - C::BM) * b_pitch + ko);
+      asm_ld16_lds(rb, dst, b_lane + (g * C::ROWS_PER_LOAD - C::BM) * b_pitch + ko);
   }
 }
 
@@ -141,7 +141,9 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   __shared__ __attribute__((aligned(1024))) char lds1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char lds2[C::STAGES > 2 ? C::STAGE : 16];
   __shared__ __attribute__((aligned(1024))) char lds3[C::STAGES > 3 ? C::STAGE : 16];
-#define WAM_GEMM_BUF(st) ((st) == 0 ? lds0 : (st) == 1 ? lds1 : (st) == 2 ? lds2 : lds3)
+  __shared__ __attribute__((aligned(1024))) char lds4[C::STAGES > 4 ? C::STAGE : 16];
+  static_assert(C::STAGES <= 5, "at most five stage objects");
+#define WAM_GEMM_BUF(st) ((st) == 0 ? lds0 : (st) == 1 ? lds1 : (st) == 2 ? lds2 : (st) == 3 ? lds3 : lds4)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WGN, wn = wave % C::WGN;
@@ -171,8 +173,8 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // chunk that the swizzle maps there.  Rows of A past M fall outside the
   // buffer resource and load as zeros.
   const uint32_t a_bytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u;
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)m0 * p.lda, a_bytes);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(W, (uint32_t)((int64_t)C::BN * p.ldw * 2));
+  const i32x4 ra = make_rsrc4(A + (int64_t)m0 * p.lda, a_bytes);
+  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)C::BN * p.ldw * 2));
   const int lrow = lane / C::KCH, pchunk = lane % C::KCH;
   // The swizzle term of row r = ROWS_PER_LOAD * g + lrow: for 128-byte rows
   // (8 rows per block) it depends on the parity of g, for 64-byte rows (16
@@ -238,6 +240,9 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
           }
           if constexpr (R < MF) __builtin_amdgcn_sched_group_barrier(0x008, MF - R, 0);
           else if constexpr (R > MF) __builtin_amdgcn_sched_group_barrier(0x100, R - MF, 0);
+        } else if constexpr (C::SCHED == 2) {
+          __builtin_amdgcn_sched_group_barrier(0x100, R, 0);   // all DS reads of step ks+1
+          __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);  // then the MFMAs of step ks
         }
       }
       // Every LDS read of this stage is done (the last step's fragments are
@@ -261,78 +266,112 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
           acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[LAST][j], fa[LAST][i], acc[j][i], 0, 0, 0);
     }
   }
-#undef WAM_GEMM_BUF
 
-  // Epilogue.  acc[j][i][4g + e] holds Y[m, n + e] with
-  //   m = m0 + wm*WTM + i*32 + l32,  n = n0 + wn*WTN + j*32 + 8g + 4*half.
+  // Epilogue, staged through LDS.  The accumulators are in MFMA layout (a
+  // lane holds one row and 4 columns per fragment), which would make every
+  // global store and residual read touch 32 rows at 16 bytes each.  Instead
+  // the fp32 tile goes to the (now idle) stage buffers, RPO rows per buffer,
+  // and is read back row-wise: a wave covers whole rows, so bias, modulation,
+  // residual and output accesses are contiguous and fill whole cache lines.
+  // Rows are 16-byte chunks XOR-swizzled by (row & 15), which keeps both the
+  // column-wise writes and the row-wise reads free of bank conflicts.
+  constexpr int RPO = (C::STAGE / (C::BN * 4)) / 32 * 32;  // fp32 rows per buffer
+  static_assert(RPO >= 32, "a stage buffer must hold 32 fp32 rows of the tile");
+  constexpr int ROUND = RPO * C::STAGES;                 // rows staged per round
+  constexpr int NROUNDS = (C::BM + ROUND - 1) / ROUND;
+  constexpr int QPR = C::BN / 4;                         // 16-byte chunks per fp32 row
+  constexpr int RPI = 64 / QPR;                          // rows per wave-wide access
+  static_assert(QPR == 64 || QPR == 32, "BN must be 256 or 128");
+  constexpr int ROW_B = C::BN * 4;
   void* out = seg == 0 ? p.out[0] : (seg == 1 ? p.out[1] : p.out[2]);
   const bf16* __restrict__ bias = seg == 0 ? p.bias[0] : (seg == 1 ? p.bias[1] : p.bias[2]);
+  const int q = lane % QPR;  // this lane's chunk of a row in the read phase
+  const int n = n0 + 4 * q;
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (bias) {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(bias + n);
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i) {
-    const int m = m0 + wm * C::WTM + i * 32 + l32;
-    if (m >= p.M) continue;
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * C::WTN + j * 32 + 8 * g + 4 * half;
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = acc[j][i][4 * g + e];
-        if (bias) {
-          bf16x4 bv = *reinterpret_cast<const bf16x4*>(bias + n);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] += static_cast<float>(bv[e]);
-        }
-        if constexpr (EPI == WAM_EPI_BIAS_GELU) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
-        } else if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
-          float rv[4];
-          const int64_t ro = (int64_t)m * p.ldr + n;
-          if (p.res_f32) {
-            const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
-            rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
-          } else {
-            const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
-          }
-          if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-            float gt[4];
-            ld_mod4(p.gate, p.seg_n, m, p.gate_index, n, gt);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
-          }
-          if (p.out_f32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * p.ldo + n) =
-                make_float4(y[0], y[1], y[2], y[3]);
-            continue;
-          }
-        }
-        bf16x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
-        *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = o;
-      }
-    }
+    for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
   }
+  __syncthreads();  // every wave is done reading the last stage
+#pragma unroll
+  for (int rd = 0; rd < NROUNDS; ++rd) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int r = wm * C::WTM + i * 32;  // first tile row of this fragment row (uniform)
+      if (r / ROUND != rd) continue;
+      const int obj = (r % ROUND) / RPO;
+      char* buf = WAM_GEMM_BUF(obj);
+      const int lr = r % RPO + l32;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int qq = (wn * C::WTN + j * 32 + 8 * g) / 4 + half;
+          const f32x4 v = {acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(buf + lr * ROW_B + ((qq ^ (lr & 15)) << 4)) = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < ROUND / (C::kWaves * RPI); ++it) {
+      const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
+      const int row = rd * ROUND + rr;
+      const int m = m0 + row;
+      if (row >= C::BM || m >= p.M) continue;
+      const int obj = rr / RPO, lr = rr % RPO;
+      const char* buf = WAM_GEMM_BUF(obj);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(buf + lr * ROW_B + ((q ^ (lr & 15)) << 4));
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = v[e] + bv[e];
+      if constexpr (EPI == WAM_EPI_BIAS_GELU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
+      } else if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
+        float rv[4];
+        const int64_t ro = (int64_t)m * p.ldr + n;
+        if (p.res_f32) {
+          const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
+          rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
+        } else {
+          const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
+        }
+        if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+          float gt[4];
+          ld_mod4(p.gate, p.seg_n, m, p.gate_index, n, gt);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
+        }
+        if (p.out_f32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * p.ldo + n) =
+              make_float4(y[0], y[1], y[2], y[3]);
+          continue;
+        }
+      }
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
+      *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = o;
+    }
+    if (rd + 1 < NROUNDS) __syncthreads();
+  }
+#undef WAM_GEMM_BUF
 }
 
 // Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
-using Cfg256x256w4 = GemmCfg<256, 256, 64, 2, 2, 2>;
 using Cfg256x256w8 = GemmCfg<256, 256, 64, 2, 4, 2>;
-using Cfg256x256k32w4 = GemmCfg<256, 256, 32, 2, 2, 4>;
-using Cfg256x256k32w8 = GemmCfg<256, 256, 32, 2, 4, 4>;
 using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
 using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
 using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
-using Cfg256x128k32w4b2 = GemmCfg<256, 128, 32, 2, 2, 3, 2>;
+using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
+using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
 using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
-using Cfg128x256k32w4b2 = GemmCfg<128, 256, 32, 2, 2, 3, 2>;
 
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
@@ -363,16 +402,13 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
 // Configuration by name (tuning override through WAM_GEMM_CFG), else by shape.
 static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool* found) {
   *found = true;
-  if (!strcmp(name, "256x256w4")) return launch_gemm<Cfg256x256w4>(p, s);
   if (!strcmp(name, "256x256w8")) return launch_gemm<Cfg256x256w8>(p, s);
-  if (!strcmp(name, "256x256k32w4")) return launch_gemm<Cfg256x256k32w4>(p, s);
-  if (!strcmp(name, "256x256k32w8")) return launch_gemm<Cfg256x256k32w8>(p, s);
   if (!strcmp(name, "256x128w4")) return launch_gemm<Cfg256x128w4>(p, s);
   if (!strcmp(name, "128x128w4")) return launch_gemm<Cfg128x128w4>(p, s);
   if (!strcmp(name, "256x256w8s")) return launch_gemm<Cfg256x256w8s>(p, s);
-  if (!strcmp(name, "256x128k32w4b2")) return launch_gemm<Cfg256x128k32w4b2>(p, s);
+  if (!strcmp(name, "256x256w8t")) return launch_gemm<Cfg256x256w8t>(p, s);
+  if (!strcmp(name, "256x256k32w8t4")) return launch_gemm<Cfg256x256k32w8t4>(p, s);
   if (!strcmp(name, "256x128k32w4b2s")) return launch_gemm<Cfg256x128k32w4b2s>(p, s);
-  if (!strcmp(name, "128x256k32w4b2")) return launch_gemm<Cfg128x256k32w4b2>(p, s);
   *found = false;
   return WAM_OK;
 }
@@ -428,7 +464,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
   const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
-  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_gemm<Cfg256x256w8s>(p, s);
+  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_gemm<Cfg256x256w8t>(p, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);

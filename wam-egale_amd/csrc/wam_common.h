@@ -83,6 +83,30 @@ __device__ inline bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+// Buffer resource as four dwords (gfx9 layout: base, base[47:32] with stride
+// 0, num_records in bytes, format dword), for use in inline assembly.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ inline i32x4 make_rsrc4(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  i32x4 r;
+  r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = (int)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// Direct-to-LDS load through inline assembly: the compiler does not see an
+// LDS write here, so it inserts no waits of its own; the caller orders the
+// load with explicit s_waitcnt vmcnt and barriers.  Lane L writes bytes
+// [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
+__device__ inline void asm_ld16_lds(i32x4 rsrc, void* lds, int voff) {
+  // The low 32 bits of a generic pointer into LDS are the LDS byte offset.
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "s"(m0) : "memory", "m0");
+}
+
 // 16 bytes per lane from a buffer resource straight into LDS: lane L writes
 // bytes [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
 __device__ inline void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
