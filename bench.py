@@ -122,6 +122,42 @@ def cpu_baseline(shape, seconds_budget=30.0):
                       f"torch threads {threads}, os.cpu_count {os.cpu_count()}, {cpu_model}"}
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "l4680_ffn1_traffic.md"
+
+
+def pmc_ffn1(shape, dev, M):
+    """Counter-pass workload: the L4680 FFN1 GEMM (LN3 output [M, 3072] x
+    W1 [14336, 3072]^T + b1, GELU) 5 times, then a plain 1 GiB device-to-device
+    copy 3 times, whose FETCH_SIZE / WRITE_SIZE calibrate the counters."""
+    import torch
+    from wam_ops import ops
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(M, shape.dim, device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(shape.ffn, shape.dim, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    b1 = torch.zeros(shape.ffn, device=dev, dtype=torch.bfloat16)
+    for _ in range(5):
+        ops.linear(x, w1, b1, epilogue=ops.EPI_BIAS_GELU)
+    torch.cuda.synchronize()
+    src = torch.ones(1 << 29, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_ffn1": "done", "copy_bytes": src.numel() * 2}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per FFN1 launch from the committed counter summary (two
+    rocprofv3 --pmc passes, each calibrated against a 1 GiB copy), or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,6 +165,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--pmc-ffn1", action="store_true",
+                    help="only launch the FFN1 GEMM 5 times and a 1 GiB device copy 3 times "
+                         "(the workload for the FETCH_SIZE / WRITE_SIZE counter passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the block on a single MI355X "
@@ -143,6 +182,10 @@ def main():
     torch.cuda.set_device(dev)
     shape = synthetic.WAN22_5B
     D, F, M, Lc = shape.dim, shape.ffn, 4680, 512
+
+    if args.pmc_ffn1:
+        pmc_ffn1(shape, dev, M)
+        return
 
     blk = build_block(shape, dev)
     x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, M, (6, 26, 30), context_len=Lc,
@@ -185,7 +228,7 @@ def main():
         "layer_flop": flops,
         "roofline": {"bound": "mfma", "kernel": "FFN1 GEMM 4680x14336x3072 + bias + GELU(tanh)",
                      "achieved": round(ffn1_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(ffn1 * 1e3, 1)},
         "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
     }

@@ -93,6 +93,10 @@ __device__ inline i32x4 make_rsrc4(const void* p, uint32_t bytes) {
   r[1] = (int)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
   r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
   r[3] = 0x00020000;
+  // The dwords may have been written by v_readfirstlane: a VMEM instruction
+  // that reads an SGPR written by a VALU needs 5 wait states in between, and
+  // the compiler does not see the loads inside inline assembly.
+  asm volatile("s_nop 4" : "+s"(r));
   return r;
 }
 
@@ -103,7 +107,8 @@ __device__ inline i32x4 make_rsrc4(const void* p, uint32_t bytes) {
 __device__ inline void asm_ld16_lds(i32x4 rsrc, void* lds, int voff) {
   // The low 32 bits of a generic pointer into LDS are the LDS byte offset.
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  // One wait state between the M0 write and the LDS DMA that reads it.
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :: "v"(voff), "s"(rsrc), "s"(m0) : "memory", "m0");
 }
 
