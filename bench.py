@@ -158,6 +158,36 @@ def measured_traffic():
     return None
 
 
+def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup, layers=30):
+    """C5: the 30-layer speculative verify forward (BlockStack) measured as a
+    whole: 30 random-init layers, each with its own 6240-token committed prefix
+    in pool row 0 and its own precomputed cross K/V; 4 candidates x 1560 tokens."""
+    import torch
+    from wam_ops import BlockStack, synthetic
+    B, Mv = x.shape[0], x.shape[1]
+    blocks = []
+    for i in range(layers):
+        blk = build_block(shape, dev, seed=100 + i)
+        blk.attn1.attn_caches["pos"] = synthetic.kv_pool(shape, prefix + Mv, prefix, batch=1,
+                                                         seed=300 + i, device=dev)
+        blocks.append(blk)
+    stack = BlockStack(blocks)
+    with torch.no_grad():
+        stack.prepare_context(ctx, precompute=True)
+
+    def run():
+        with torch.no_grad():
+            return stack(x, ctx, temb, freqs, candidate_cache_rows=rows)
+    ms = timed_steps(run, steps, warmup)
+    g, a = layer_flops(Mv, shape.dim, shape.ffn, ctx.shape[1], self_keys=prefix + Mv, batch=B)
+    res = {"layers": layers, "ms_per_forward": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
+           "tokens_per_s": round(B * Mv / (ms * 1e-3), 1),
+           "tflops": round(layers * (g + a) / (ms * 1e-3) / 1e12, 1), "steps": steps, "warmup": warmup}
+    del stack, blocks
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,7 +284,10 @@ def main():
                           "tokens_per_s": round(B * Mv / (vms * 1e-3), 1),
                           "tflops": round((g + a) / (vms * 1e-3) / 1e12, 1),
                           "frac_of_bf16_peak": round((g + a) / (vms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                          "us_30_layers": round(30 * vms * 1e3, 1)}
+                          "us_30_layers_extrapolated": round(30 * vms * 1e3, 1)}
+        del vlayer
+        out["lverify"]["stack30"] = verify_stack30(shape, dev, xv, ctxv, tembv, freqv, rows, prefix,
+                                                   min(args.steps, 5), 2)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

@@ -134,3 +134,21 @@ def test_prepare_context_groups_identical_rows():
     assert wl.context_roots.tolist() == [0, 1, 3]
     wl.prepare_context(ctx[:2].clone(), precompute=False)
     assert wl.context_rows is None
+
+
+def test_block_stack_contract_on_host():
+    """The verify stack refuses a writing update with candidate rows and a
+    missing read-only cache before any native call (model.py:1056-1057, :628-629)."""
+    from wam_ops import BlockStack
+    blocks = [TransformerBlock(64, 128, 2, cross_attn_norm=True) for _ in range(2)]
+    stack = BlockStack(blocks)
+    assert len(stack) == 2
+    x = torch.zeros(2, 4, 64, dtype=torch.bfloat16)
+    rows = torch.zeros(2, dtype=torch.int64)
+    with torch.no_grad():
+        with pytest.raises(ValueError, match="update_cache=0"):
+            stack(x, x, None, None, update_cache=1, candidate_cache_rows=rows)
+        with pytest.raises(ValueError, match="read-only KV"):
+            stack(x, x, None, None, candidate_cache_rows=rows)
+    with pytest.raises(ValueError):
+        BlockStack([])

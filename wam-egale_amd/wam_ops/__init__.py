@@ -8,8 +8,9 @@ TransformerBlock / Attention parameter containers, and per-stage operators in
 from .install import install_block, install_model
 from .native import NativeBlock
 from .whole_layer import WholeLayerBlock
+from .verify import BlockStack
 from .block import TransformerBlock
 from .parameters import Attention
 
-__all__ = ["install_block", "install_model", "NativeBlock", "WholeLayerBlock",
+__all__ = ["install_block", "install_model", "NativeBlock", "WholeLayerBlock", "BlockStack",
            "TransformerBlock", "Attention"]

@@ -81,8 +81,13 @@ def validate_candidate_rows(rows, batch, pool_batch, device):
 
 def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cache,
               update_cache, candidate_cache_rows, debug=False, cross_kv=None,
-              context_rows=None, timer=None):
-    """One wam_block_forward call.  Returns the output, or (output, debug dict)."""
+              context_rows=None, timer=None, rows_checked=False, workspace=None, out=None):
+    """One wam_block_forward call.  Returns the output, or (output, debug dict).
+
+    ``rows_checked``: the caller has already validated the candidate rows'
+    values against this cache's batch (no host read-back here).
+    ``workspace``: a uint8 device tensor to use if it is large enough.
+    ``out``: a preallocated [B, M, D] bf16 output (must not alias the input)."""
     x = hidden_states
     dev = bound.device
     _check(x.is_cuda and x.device == dev and x.dtype == torch.bfloat16 and x.is_contiguous()
@@ -130,7 +135,12 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
         if candidate_cache_rows is not None:
             if update_cache != 0:
                 raise ValueError("candidate verification requires existing read-only KV")
-            validate_candidate_rows(candidate_cache_rows, B, k.shape[0], dev)
+            if rows_checked:
+                _check(candidate_cache_rows.ndim == 1 and candidate_cache_rows.numel() == B
+                       and candidate_cache_rows.dtype == torch.long
+                       and candidate_cache_rows.device == dev, "candidate_cache_rows schema")
+            else:
+                validate_candidate_rows(candidate_cache_rows, B, k.shape[0], dev)
             args.candidate_rows = candidate_cache_rows.data_ptr()
         elif k.shape[0] != B:
             raise RuntimeError(f"KV branch contract: cache batch {k.shape[0]} != {B}")
@@ -139,11 +149,19 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     args.update = int(update_cache)
     if cross_kv is not None:
         args.cross_k, args.cross_v = cross_kv[0].data_ptr(), cross_kv[1].data_ptr()
-    out = torch.empty_like(x)
+    if out is None:
+        out = torch.empty_like(x)
+    else:
+        _check(out.shape == x.shape and out.dtype == x.dtype and out.device == dev
+               and out.is_contiguous() and out.data_ptr() != x.data_ptr(),
+               "out must be a separate [B, M, D] bf16 tensor")
     args.out = out.data_ptr()
     nbytes = _lib.lib().wam_block_workspace_bytes(B, M, D, bound.ffn_dim, ctx.shape[0],
                                                    ctx.shape[1], pool)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if workspace is not None and workspace.numel() >= nbytes and workspace.device == dev:
+        ws = workspace
+    else:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
     dbg = None
     if debug:

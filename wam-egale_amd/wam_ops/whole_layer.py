@@ -66,7 +66,7 @@ class WholeLayerBlock:
 
     def __call__(self, hidden_states, encoder_hidden_states, temb, rotary_emb,
                  update_cache=0, cache_name="pos", candidate_cache_rows=None, debug=False,
-                 timer=None):
+                 timer=None, rows_checked=False, workspace=None, out=None):
         if torch.is_grad_enabled():
             raise RuntimeError("WholeLayerBlock is inference-only; use no_grad/inference_mode")
         caches = self.block.attn1.attn_caches or {}
@@ -81,7 +81,7 @@ class WholeLayerBlock:
             ctx = encoder_hidden_states.index_select(0, self.context_roots).contiguous()
         res = run_block(self.bound(), hidden_states, ctx, temb, rotary_emb, cache, update_cache,
                         candidate_cache_rows, debug=debug, cross_kv=cross_kv, context_rows=rows,
-                        timer=timer)
+                        timer=timer, rows_checked=rows_checked, workspace=workspace, out=out)
         if debug:
             return res[1]
         return res
