@@ -47,10 +47,15 @@ def test_linear_bias(dev, M, K, N, nseg):
         assert_close(o, ref, max_abs=bound, min_cos=0.99999, what=f"linear {M}x{K}x{N}")
 
 
-@pytest.mark.parametrize("M", [130, 4680])
-def test_linear_epilogues(dev, M):
+# (4680, 256, 3584) and (4680, 256, 14336) have 266 and 1064 256x256 tiles:
+# just above a multiple of the 256 CUs, so their last columns run as a second
+# 128x128-tile launch (column offsets into bias, residual, output and the
+# modulation table).
+@pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
+                                   (4680, 256, 14336)])
+def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
-    K, N, D = 1024, 2048, 2048
+    D = N
     x = _randn((M, K), dev, 2)
     w = _randn((N, K), dev, 3, 0.05)
     b = _randn((N,), dev, 4, 0.05)

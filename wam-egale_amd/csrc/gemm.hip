@@ -28,6 +28,8 @@ struct LinearParams {
   int epi;
   const void* res; int64_t ldr; int res_f32, out_f32;
   wam_modulation gate; int gate_index;
+  int mod_d;   // row length of the modulation table (the full output width)
+  int n_off;   // column of this launch's first output column in that table
 };
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0>
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
         }
         if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
           float gt[4];
-          ld_mod4(p.gate, p.seg_n, m, p.gate_index, n, gt);
+          ld_mod4(p.gate, p.mod_d, m, p.gate_index, n + p.n_off, gt);
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
         } else {
@@ -413,6 +415,49 @@ static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool
   return WAM_OK;
 }
 
+static int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// 256x256 tiles run in whole-chip rounds (one workgroup per CU).  When the
+// tile count is just above a multiple of the CU count, the last round keeps
+// most CUs idle: the output columns of that partial round go to a second
+// launch with 128x128 tiles, which spreads them over the whole chip.
+static int launch_big(LinearParams& p, hipStream_t s) {
+  const int cus = cu_count();
+  const int mt = (p.M + 255) / 256, nt = p.seg_n / 256;
+  const int64_t tiles = (int64_t)mt * nt;
+  const int64_t full = tiles / cus, rem = tiles - full * cus;
+  if (p.n_seg_count == 1 && full >= 1 && rem > 0 && rem * 4 < cus) {
+    const int n_main = (int)(full * cus / mt);
+    const int tail_cols = (nt - n_main) * 256;
+    const int64_t small = (int64_t)((p.M + 127) / 128) * (tail_cols / 128);
+    if (n_main >= 1 && tail_cols > 0 && small <= cus) {
+      LinearParams main = p;
+      main.seg_n = n_main * 256;
+      WAM_TRY(launch_gemm<Cfg256x256w8t>(main, s));
+      LinearParams tail = p;
+      const int64_t c0 = (int64_t)n_main * 256;
+      tail.seg_n = tail_cols;
+      tail.n_off = p.n_off + (int)c0;
+      tail.w[0] = p.w[0] + c0 * p.ldw;
+      tail.bias[0] = p.bias[0] ? p.bias[0] + c0 : nullptr;
+      tail.out[0] = static_cast<char*>(p.out[0]) + c0 * (p.out_f32 ? 4 : 2);
+      if (p.res) tail.res = static_cast<const char*>(p.res) + c0 * (p.res_f32 ? 4 : 2);
+      return launch_gemm<Cfg128x128w4>(tail, s);
+    }
+  }
+  return launch_gemm<Cfg256x256w8t>(p, s);
+}
+
 int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a != nullptr, "wam_linear: null args");
   WAM_REQUIRE(a->n_seg >= 1 && a->n_seg <= 3, "wam_linear: n_seg must be 1..3 (got %d)", a->n_seg);
@@ -455,6 +500,8 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.out_f32 = a->out_dtype == WAM_F32;
   p.gate = a->gate; p.gate_index = a->gate_index;
   p.n_seg_count = a->n_seg;
+  p.mod_d = a->seg_n;
+  p.n_off = 0;
   const char* force = getenv("WAM_GEMM_CFG");
   if (force && *force) {
     bool found = false;
@@ -464,7 +511,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
   const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
-  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_gemm<Cfg256x256w8t>(p, s);
+  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big(p, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);

@@ -112,6 +112,13 @@ __device__ inline void asm_ld16_lds(i32x4 rsrc, void* lds, int voff) {
                :: "v"(voff), "s"(rsrc), "s"(m0) : "memory", "m0");
 }
 
+// Same for a per-lane 64-bit global address (global_load_lds_dwordx4).
+__device__ inline void asm_g_ld16_lds(uint64_t gaddr, void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(gaddr), "s"(m0) : "memory", "m0");
+}
+
 // 16 bytes per lane from a buffer resource straight into LDS: lane L writes
 // bytes [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
 __device__ inline void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
