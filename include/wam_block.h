@@ -61,7 +61,7 @@ enum {
 };
 
 /* Element types; zero (a memset struct) means bf16. */
-enum { WAM_BF16 = 0, WAM_F32 = 1 };
+enum { WAM_BF16 = 0, WAM_F32 = 1, WAM_FP8 = 2 /* OCP e4m3 (e4m3fn), weights only */ };
 
 /* Epilogues of wam_linear. */
 enum {
@@ -90,7 +90,7 @@ typedef struct {
   int M, K;
   int n_seg;         /* 1..3 output segments (QKV runs as one launch) */
   int seg_n;         /* columns per segment */
-  const void* w[3];  /* [seg_n, K] bf16 each, row stride ldw */
+  const void* w[3];  /* [seg_n, K] bf16 (or fp8, w_dtype) each, row stride ldw elements */
   int64_t ldw;
   const void* bias[3]; /* [seg_n] bf16 each, or NULL */
   void* out[3];      /* [M, seg_n] bf16 each, row stride ldo */
@@ -102,9 +102,24 @@ typedef struct {
   int out_dtype;     /* WAM_BF16 | WAM_F32 (f32 only for the residual epilogues) */
   wam_modulation gate; /* gate row = mod[b, t, gate_index] for row m = b*tokens+t */
   int gate_index;
+  /* Weight storage.  WAM_BF16, or WAM_FP8: e4m3 weights with one fp32 scale
+   * per output column (w_scale[s][n], typically absmax/448 of the bf16 row):
+   * acc = sum_k a[m,k] * fp8(w[n,k]) is scaled by w_scale[n] before the bias.
+   * This is the fp8-weight / bf16-activation FFN variant; the reference has
+   * no fp8 path. */
+  int w_dtype;
+  const float* w_scale[3];
 } wam_linear_args;
 
 int wam_linear(const wam_linear_args* args, void* stream);
+
+/* Per-row fp8 quantization of a bf16 matrix w [rows, cols] (row stride ldw):
+ * scale[r] = max_c |w[r,c]| / 448 (1 for an all-zero row) and
+ * q[r, c] = e4m3(w[r,c] / scale[r]), round to nearest even (q row stride cols).
+ * Prepares the fp8 weights of wam_linear (w_dtype = WAM_FP8).  No counterpart
+ * in the reference, which has no fp8 path. */
+int wam_quantize_fp8_rows(const void* w, int rows, int cols, int64_t ldw, void* q, float* scale,
+                          void* stream);
 
 /* ----------------------------------------------------------- LayerNorm */
 /* y = bf16(LN(x) * (1 + mod[shift+1]) + mod[shift])   when affine == 0

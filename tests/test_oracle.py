@@ -160,3 +160,34 @@ def test_bf16_reference_vs_fp32_calibration():
     ref16 = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps, dtype=torch.bfloat16)
     m = compare(ref16, ref32)
     assert m["cosine"] > 0.99999 and m["max_abs"] < 0.05
+
+
+def test_fp8_quantization_pinned():
+    """The oracle's e4m3 quantization against values decoded by hand from the
+    OCP E4M3 bit layout, exact round-to-nearest-even cases and the per-row
+    scale's closed form."""
+    from oracle import fp8
+    # every finite e4m3 byte decodes to a value that the cast maps back to itself
+    for b in range(256):
+        v = fp8.e4m3_decode(b)
+        if v != v:  # NaN codes 0x7f, 0xff
+            continue
+        t = torch.tensor([v], dtype=torch.float32).to(fp8.E4M3)
+        assert t.view(torch.uint8).item() in (b, 0x00 if b == 0x80 else b), (b, v)
+        assert t.float().item() == v
+    assert fp8.e4m3_decode(0x7E) == 448.0 and fp8.e4m3_decode(0x38) == 1.0
+    assert fp8.e4m3_decode(0x01) == 2.0 ** -9  # smallest subnormal
+    # round to nearest even between neighbours 1.0 (0x38) and 1.125 (0x39)
+    cases = {1.0625: 0x38, 1.0625 + 1e-3: 0x39, 1.1875: 0x3A, 1.1875 - 1e-3: 0x39, 447.0: 0x7E}
+    for v, b in cases.items():
+        assert torch.tensor([v]).to(fp8.E4M3).view(torch.uint8).item() == b, v
+    # per-row scale: the row max maps to 448 exactly, zero rows get scale 1
+    w = torch.tensor([[0.5, -2.0, 1.0, 0.0], [0.0, 0.0, 0.0, 0.0], [3e-3, -1e-3, 2e-3, 7e-4]])
+    q, s = fp8.quantize_rows(w)
+    assert torch.allclose(s, torch.tensor([2.0 / 448, 1.0, 3e-3 / 448]))
+    assert q.float()[0, 1].item() == -448.0 and q.float()[2, 0].item() == 448.0
+    assert q.float()[1].abs().sum().item() == 0.0
+    deq = fp8.dequantize_rows(q, s)
+    # relative error of a normal e4m3 value is at most 2^-4 (3 mantissa bits, RNE)
+    nz = w.abs() > 0
+    assert ((deq - w).abs()[nz] <= w.abs()[nz] * 2 ** -4 + 1e-12).all()

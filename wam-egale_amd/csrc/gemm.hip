@@ -22,19 +22,22 @@ namespace wam {
 struct LinearParams {
   const bf16* a; int64_t lda; int M, K;
   int seg_n, n_tiles_per_seg, m_tiles, n_tiles, n_seg_count;
-  const bf16* w[3]; int64_t ldw;
+  const void* w[3]; int64_t ldw;      // ldw in elements of the weight dtype
   const bf16* bias[3];
   void* out[3]; int64_t ldo;
   int epi;
   const void* res; int64_t ldr; int res_f32, out_f32;
   wam_modulation gate; int gate_index;
+  const float* wscale[3];  // per-output-column fp32 scales of fp8 weights (else unused)
   int mod_d;   // row length of the modulation table (the full output width)
   int n_off;   // column of this launch's first output column in that table
 };
 
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0>
+template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0,
+          int WB_ = 2>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+  static constexpr int WB = WB_;          // bytes per weight element: 2 (bf16) or 1 (fp8 e4m3)
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
   static constexpr int SCHED = SCHED_;    // 1: alternate DS reads and MFMAs; 2: all reads of
                                           // the next k-step, then this step's MFMAs
@@ -44,14 +47,19 @@ struct GemmCfg {
   static constexpr int TM = WTM / 32, TN = WTN / 32;
   static constexpr int KCH = BK / 8;                     // 16-byte chunks per LDS row
   static constexpr int ROW_BYTES = BK * 2;
-  static constexpr int A_BYTES = BM * ROW_BYTES, B_BYTES = BN * ROW_BYTES;
+  static constexpr int W_ROW_BYTES = BK * WB;
+  static constexpr int KCH_W = W_ROW_BYTES / 16;         // 16-byte chunks per LDS weight row
+  static constexpr int A_BYTES = BM * ROW_BYTES, B_BYTES = BN * W_ROW_BYTES;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int ROWS_PER_LOAD = 1024 / ROW_BYTES;  // one wave-wide 16 B/lane load
-  static constexpr int LOADS = (BM + BN) / ROWS_PER_LOAD;  // per stage, whole workgroup
+  static constexpr int ROWS_PER_LOAD = 1024 / ROW_BYTES;    // A rows per wave-wide 16 B/lane load
+  static constexpr int W_ROWS_PER_LOAD = 1024 / W_ROW_BYTES;
+  static constexpr int A_LOADS = BM / ROWS_PER_LOAD, W_LOADS = BN / W_ROWS_PER_LOAD;
+  static constexpr int LOADS = A_LOADS + W_LOADS;          // per stage, whole workgroup
   static constexpr int LOADS_PER_WAVE = LOADS / kWaves;
   static_assert(KCH == 8 || KCH == 4, "BK must be 64 or 32");
-  static_assert(LOADS % kWaves == 0 && BM % ROWS_PER_LOAD == 0, "load split");
-  static_assert((BM / ROWS_PER_LOAD) % kWaves == 0 && kWaves % 2 == 0, "loads per wave: A then W");
+  static_assert(WB == 2 || (WB == 1 && BK == 64), "fp8 weights use 64-deep k-steps");
+  static_assert(A_LOADS % kWaves == 0 && W_LOADS % kWaves == 0 && kWaves % 2 == 0,
+                "loads per wave: A then W");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(STAGES >= 2 && BLOCKS * (STAGES * STAGE + (5 - STAGES) * 1024) <= 160 * 1024, "LDS budget");
 };
@@ -109,8 +117,8 @@ __device__ inline void wait_vmcnt() {
 template <class C>
 __device__ __forceinline__ void issue_stage(char* base, i32x4 ra, i32x4 rb, int wave, int a_lane,
                                             int b_lane, int a_pitch, int b_pitch, int kt) {
-  const int ko = kt * C::BK * 2;
-  constexpr int A_ITERS = C::BM / C::ROWS_PER_LOAD / C::kWaves;
+  const int ko = kt * C::BK * 2, ko_w = kt * C::BK * C::WB;
+  constexpr int A_ITERS = C::A_LOADS / C::kWaves;
 #pragma unroll
   for (int i = 0; i < C::LOADS_PER_WAVE; ++i) {
     const int g = wave + i * C::kWaves;
@@ -118,7 +126,7 @@ __device__ __forceinline__ void issue_stage(char* base, i32x4 ra, i32x4 rb, int 
     if (i < A_ITERS)
       asm_ld16_lds(ra, dst, a_lane + g * C::ROWS_PER_LOAD * a_pitch + ko);
     else
-      asm_ld16_lds(rb, dst, b_lane + (g * C::ROWS_PER_LOAD - C::BM) * b_pitch + ko);
+      asm_ld16_lds(rb, dst, b_lane + (g - C::A_LOADS) * C::W_ROWS_PER_LOAD * b_pitch + ko_w);
   }
 }
 
@@ -130,8 +138,18 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
   for (int i = 0; i < C::TM; ++i)
     fa[i] = ld_bf16x8(abase + lds_off<C::KCH>(wm * C::WTM + i * 32 + l32, c));
 #pragma unroll
-  for (int j = 0; j < C::TN; ++j)
-    fb[j] = ld_bf16x8(bbase + lds_off<C::KCH>(wn * C::WTN + j * 32 + l32, c));
+  for (int j = 0; j < C::TN; ++j) {
+    const int r = wn * C::WTN + j * 32 + l32;
+    if constexpr (C::WB == 2) {
+      fb[j] = ld_bf16x8(bbase + lds_off<C::KCH>(r, c));
+    } else {
+      // 8 fp8 weights (8 bytes: half c & 1 of 16-byte chunk c >> 1 of a
+      // 64-byte row), widened exactly to bf16; the per-column scale is
+      // applied to the accumulator in the epilogue.
+      const u32x2 q = *reinterpret_cast<const u32x2*>(bbase + lds_off<4>(r, c >> 1) + (c & 1) * 8);
+      fb[j] = fp8x8_to_bf16x8(q);
+    }
+  }
 }
 
 template <class C, int EPI>
@@ -165,8 +183,8 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   const int m0 = tm * C::BM;
 
   const bf16* A = p.a;
-  const bf16* wseg = seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]);
-  const bf16* W = wseg + (int64_t)n0 * p.ldw;
+  const char* wseg = static_cast<const char*>(seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]));
+  const char* W = wseg + (int64_t)n0 * p.ldw * C::WB;
 
   // Direct-to-LDS staging.  Load g (0 <= g < LOADS) of a stage fills the
   // 1 KB LDS block g, i.e. rows ROWS_PER_LOAD*g .. +ROWS_PER_LOAD of the
@@ -176,7 +194,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // buffer resource and load as zeros.
   const uint32_t a_bytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u;
   const i32x4 ra = make_rsrc4(A + (int64_t)m0 * p.lda, a_bytes);
-  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)C::BN * p.ldw * 2));
+  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)C::BN * p.ldw * C::WB));
   const int lrow = lane / C::KCH, pchunk = lane % C::KCH;
   // The swizzle term of row r = ROWS_PER_LOAD * g + lrow: for 128-byte rows
   // (8 rows per block) it depends on the parity of g, for 64-byte rows (16
@@ -187,9 +205,16 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   const int chunk1 = C::KCH == 8 ? (pchunk ^ ((r1 >> 1) & 7)) : (pchunk ^ ((r1 >> 2) & 3));
   const int lchunk = (wave & 1) ? chunk1 : chunk0;
   const int a_lane = (lrow * (int)p.lda + lchunk * 8) * 2;
-  const int b_lane = (lrow * (int)p.ldw + lchunk * 8) * 2;
-
-  const int a_pitch = (int)p.lda * 2, b_pitch = (int)p.ldw * 2;
+  const int a_pitch = (int)p.lda * 2, b_pitch = (int)p.ldw * C::WB;
+  int b_lane;
+  if constexpr (C::WB == 2) {
+    b_lane = lrow * b_pitch + lchunk * 16;
+  } else {
+    // 64-byte weight rows, 16 per block: the swizzle term (r >> 2) & 3 of row
+    // r = 16 g + lane / 4 depends on the lane only.
+    const int wrow = lane >> 2, wch = (lane & 3) ^ ((wrow >> 2) & 3);
+    b_lane = wrow * b_pitch + wch * 16;
+  }
 
   f32x16 acc[C::TN][C::TM];
 #pragma unroll
@@ -295,6 +320,12 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 #pragma unroll
     for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
   }
+  float wsc[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (C::WB == 1) {
+    const float* ws = seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2]);
+    const float4 t = *reinterpret_cast<const float4*>(ws + n);
+    wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
+  }
   __syncthreads();  // every wave is done reading the last stage
 #pragma unroll
   for (int rd = 0; rd < NROUNDS; ++rd) {
@@ -326,7 +357,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       const f32x4 v = *reinterpret_cast<const f32x4*>(buf + lr * ROW_B + ((q ^ (lr & 15)) << 4));
       float y[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = v[e] + bv[e];
+      for (int e = 0; e < 4; ++e) y[e] = C::WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
       if constexpr (EPI == WAM_EPI_BIAS_GELU) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
@@ -374,6 +405,9 @@ using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
 using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
 using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
 using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
+// fp8 e4m3 weights (64-byte LDS weight rows, three stages)
+using Cfg256x256f8 = GemmCfg<256, 256, 64, 2, 4, 3, 1, 2, 1>;
+using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
 
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
@@ -431,6 +465,7 @@ static int cu_count() {
 // tile count is just above a multiple of the CU count, the last round keeps
 // most CUs idle: the output columns of that partial round go to a second
 // launch with 128x128 tiles, which spreads them over the whole chip.
+template <class CBig, class CSmall>
 static int launch_big(LinearParams& p, hipStream_t s) {
   const int cus = cu_count();
   const int mt = (p.M + 255) / 256, nt = p.seg_n / 256;
@@ -443,19 +478,20 @@ static int launch_big(LinearParams& p, hipStream_t s) {
     if (n_main >= 1 && tail_cols > 0 && small <= cus) {
       LinearParams main = p;
       main.seg_n = n_main * 256;
-      WAM_TRY(launch_gemm<Cfg256x256w8t>(main, s));
+      WAM_TRY(launch_gemm<CBig>(main, s));
       LinearParams tail = p;
       const int64_t c0 = (int64_t)n_main * 256;
       tail.seg_n = tail_cols;
       tail.n_off = p.n_off + (int)c0;
-      tail.w[0] = p.w[0] + c0 * p.ldw;
+      tail.w[0] = static_cast<const char*>(p.w[0]) + c0 * p.ldw * CBig::WB;
+      if (p.wscale[0]) tail.wscale[0] = p.wscale[0] + c0;
       tail.bias[0] = p.bias[0] ? p.bias[0] + c0 : nullptr;
       tail.out[0] = static_cast<char*>(p.out[0]) + c0 * (p.out_f32 ? 4 : 2);
       if (p.res) tail.res = static_cast<const char*>(p.res) + c0 * (p.res_f32 ? 4 : 2);
-      return launch_gemm<Cfg128x128w4>(tail, s);
+      return launch_gemm<CSmall>(tail, s);
     }
   }
-  return launch_gemm<Cfg256x256w8t>(p, s);
+  return launch_gemm<CBig>(p, s);
 }
 
 int linear(const wam_linear_args* a, hipStream_t s) {
@@ -465,13 +501,18 @@ int linear(const wam_linear_args* a, hipStream_t s) {
               a->M, a->K, a->seg_n);
   WAM_REQUIRE(a->K % 64 == 0, "wam_linear: K=%d must be a multiple of 64", a->K);
   WAM_REQUIRE(a->seg_n % 128 == 0, "wam_linear: N=%d must be a multiple of 128", a->seg_n);
-  WAM_REQUIRE(a->lda % 8 == 0 && a->ldw % 8 == 0 && a->ldo % 4 == 0,
+  WAM_REQUIRE(a->w_dtype == WAM_BF16 || a->w_dtype == WAM_FP8, "wam_linear: w_dtype %d", a->w_dtype);
+  const bool f8 = a->w_dtype == WAM_FP8;
+  const int wb = f8 ? 1 : 2;
+  WAM_REQUIRE(a->lda % 8 == 0 && (a->ldw * wb) % 16 == 0 && a->ldo % 4 == 0,
               "wam_linear: row strides must keep 16-byte alignment");
   WAM_REQUIRE(a->a != nullptr, "wam_linear: null activation");
-  WAM_REQUIRE((int64_t)a->M * a->lda * 2 < (int64_t)1 << 31 && (int64_t)a->seg_n * a->ldw * 2 < (int64_t)1 << 31,
+  WAM_REQUIRE((int64_t)a->M * a->lda * 2 < (int64_t)1 << 31 && (int64_t)a->seg_n * a->ldw * wb < (int64_t)1 << 31,
               "wam_linear: operands above 2 GiB are not supported");
-  for (int i = 0; i < a->n_seg; ++i)
+  for (int i = 0; i < a->n_seg; ++i) {
     WAM_REQUIRE(a->w[i] != nullptr && a->out[i] != nullptr, "wam_linear: null weight/out %d", i);
+    WAM_REQUIRE(!f8 || a->w_scale[i] != nullptr, "wam_linear: fp8 weights need w_scale %d", i);
+  }
   WAM_REQUIRE(a->epilogue >= WAM_EPI_BIAS && a->epilogue <= WAM_EPI_BIAS_RES,
               "wam_linear: unknown epilogue %d", a->epilogue);
   WAM_REQUIRE((a->res_dtype == WAM_BF16 || a->res_dtype == WAM_F32) &&
@@ -491,7 +532,8 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.seg_n = a->seg_n; p.ldw = a->ldw; p.ldo = a->ldo; p.epi = a->epilogue;
   for (int i = 0; i < 3; ++i) {
     const int j = i < a->n_seg ? i : 0;
-    p.w[i] = static_cast<const bf16*>(a->w[j]);
+    p.w[i] = a->w[j];
+    p.wscale[i] = f8 ? a->w_scale[j] : nullptr;
     p.bias[i] = static_cast<const bf16*>(a->bias[j]);
     p.out[i] = a->out[j];
   }
@@ -502,6 +544,11 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.n_seg_count = a->n_seg;
   p.mod_d = a->seg_n;
   p.n_off = 0;
+  const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
+  if (f8) {
+    if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256f8, Cfg128x128f8>(p, s);
+    return launch_gemm<Cfg128x128f8>(p, s);
+  }
   const char* force = getenv("WAM_GEMM_CFG");
   if (force && *force) {
     bool found = false;
@@ -510,14 +557,61 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return rc;
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
-  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big(p, s);
+  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256w8t, Cfg128x128w4>(p, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);
 }
 
+// Per-row fp8 e4m3 quantization: one workgroup per row.
+__global__ __launch_bounds__(256) void quantize_fp8_rows_kernel(const bf16* __restrict__ w, int cols,
+                                                                int64_t ldw, uint8_t* __restrict__ q,
+                                                                float* __restrict__ scale) {
+  __shared__ unsigned smax;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const bf16* row = w + (int64_t)r * ldw;
+  if (tid == 0) smax = 0u;
+  __syncthreads();
+  float mx = 0.f;
+  for (int c = tid * 8; c < cols; c += 256 * 8) {
+    const bf16x8 v = ld_bf16x8(row + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(static_cast<float>(v[e])));
+  }
+  atomicMax(&smax, __float_as_uint(mx));  // non-negative floats order as their bits
+  __syncthreads();
+  const float amax = __uint_as_float(smax);
+  const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+  uint8_t* qrow = q + (int64_t)r * cols;
+  for (int c = tid * 8; c < cols; c += 256 * 8) {
+    const bf16x8 v = ld_bf16x8(row + c);
+    int lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[0]) / sc, static_cast<float>(v[1]) / sc, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[2]) / sc, static_cast<float>(v[3]) / sc, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[4]) / sc, static_cast<float>(v[5]) / sc, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[6]) / sc, static_cast<float>(v[7]) / sc, hi, true);
+    *reinterpret_cast<u32x2*>(qrow + c) = u32x2{(unsigned)lo, (unsigned)hi};
+  }
+  if (tid == 0) scale[r] = sc;
+}
+
+int quantize_fp8_rows(const void* w, int rows, int cols, int64_t ldw, void* q, float* scale, hipStream_t s) {
+  WAM_REQUIRE(w && q && scale, "wam_quantize_fp8_rows: null pointer");
+  WAM_REQUIRE(rows >= 1 && cols >= 8 && cols % 8 == 0 && ldw % 8 == 0 && ldw >= cols,
+              "wam_quantize_fp8_rows: rows=%d cols=%d ldw=%lld (cols and ldw multiples of 8)", rows, cols,
+              (long long)ldw);
+  hipLaunchKernelGGL(quantize_fp8_rows_kernel, dim3(rows), dim3(256), 0, s, static_cast<const bf16*>(w), cols,
+                     ldw, static_cast<uint8_t*>(q), scale);
+  WAM_LAUNCHED("quantize_fp8_rows_kernel");
+  return WAM_OK;
+}
+
 }  // namespace wam
+
+extern "C" int wam_quantize_fp8_rows(const void* w, int rows, int cols, int64_t ldw, void* q, float* scale,
+                                     void* stream) {
+  return wam::quantize_fp8_rows(w, rows, cols, ldw, q, scale, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int wam_linear(const wam_linear_args* args, void* stream) {
   return wam::linear(args, static_cast<hipStream_t>(stream));

@@ -83,6 +83,20 @@ __device__ inline bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Eight OCP fp8 e4m3 values (bytes 0..7 of q) widened to bf16 (exact: every
+// e4m3 value is a bf16 value).  v_cvt_scalef32_pk_bf16_fp8 with scale 1.0
+// converts the two bytes of one 16-bit half.
+__device__ inline bf16x8 fp8x8_to_bf16x8(u32x2 q) {
+  const bf16x2 c0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, false);
+  const bf16x2 c1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, true);
+  const bf16x2 c2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, false);
+  const bf16x2 c3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, true);
+  return bf16x8{c0[0], c0[1], c1[0], c1[1], c2[0], c2[1], c3[0], c3[1]};
+}
+
 // Buffer resource as four dwords (gfx9 layout: base, base[47:32] with stride
 // 0, num_records in bytes, format dword), for use in inline assembly.
 typedef int i32x4 __attribute__((ext_vector_type(4)));

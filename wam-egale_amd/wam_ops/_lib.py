@@ -15,7 +15,7 @@ LIB_NAME = "libwam_block.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 WAM_OK, WAM_ERR_ARG, WAM_ERR_HIP, WAM_ERR_STATE = 0, -1, -2, -3
-WAM_BF16, WAM_F32 = 0, 1
+WAM_BF16, WAM_F32, WAM_FP8 = 0, 1, 2
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATE_RES, EPI_BIAS_RES = 0, 1, 2, 3
 DEBUG_SLOTS = 16
 STAGES = ("ln1", "qkv", "rms_rope", "kv_layout", "self_attn", "self_out", "ln2",
@@ -37,7 +37,8 @@ class LinearArgs(Structure):
                 ("bias", c_void_p * 3), ("out", c_void_p * 3), ("ldo", c_int64),
                 ("epilogue", c_int), ("res", c_void_p), ("ldr", c_int64),
                 ("res_dtype", c_int), ("out_dtype", c_int),
-                ("gate", Modulation), ("gate_index", c_int)]
+                ("gate", Modulation), ("gate_index", c_int),
+                ("w_dtype", c_int), ("w_scale", c_void_p * 3)]
 
 
 class LnArgs(Structure):
@@ -105,6 +106,7 @@ STRUCTS = {
 # Every symbol include/wam_block.h declares, with its ctypes signature.
 SIGNATURES = {
     "wam_linear": (c_int, [POINTER(LinearArgs), c_void_p]),
+    "wam_quantize_fp8_rows": (c_int, [c_void_p, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
     "wam_ln_modulate": (c_int, [POINTER(LnArgs), c_void_p]),
     "wam_rms_rope": (c_int, [POINTER(RmsRopeArgs), c_void_p]),
     "wam_attention": (c_int, [POINTER(AttentionArgs), c_void_p]),

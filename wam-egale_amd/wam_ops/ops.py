@@ -72,27 +72,61 @@ def modulation(table, temb, tokens):
     return m
 
 
+FP8 = torch.float8_e4m3fn
+
+
+def quantize_fp8_rows(w, out=None, scale=None):
+    """Per-row e4m3 weights: scale[r] = max|w[r]| / 448, q = e4m3(w / scale)
+    (round to nearest even).  Returns (q [rows, cols] float8_e4m3fn, scale fp32)."""
+    dev = _dev(w)
+    _bf16(w, "w")
+    _req(w.dim() == 2 and w.stride(-1) == 1, "w must be [rows, cols] with contiguous rows")
+    rows, cols = w.shape
+    q = out if out is not None else torch.empty(rows, cols, dtype=FP8, device=dev)
+    sc = scale if scale is not None else torch.empty(rows, dtype=torch.float32, device=dev)
+    _req(q.dtype == FP8 and q.is_contiguous() and q.shape == (rows, cols), "q must be [rows, cols] e4m3")
+    _req(sc.dtype == torch.float32 and sc.is_contiguous() and sc.numel() == rows, "scale must be [rows] fp32")
+    _lib.check(_lib.lib().wam_quantize_fp8_rows(w.data_ptr(), rows, cols, w.stride(0), q.data_ptr(),
+                                                 sc.data_ptr(), stream_handle(dev)), "wam_quantize_fp8_rows")
+    return q, sc
+
+
 def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=None,
-           temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16):
+           temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16, w_scale=None):
     """Y = epilogue(x W^T + b) on MFMA.  weights: one tensor or a list of up to 3
     (one launch, outputs split per weight).  Returns a tensor or a list.
     The residual may be bf16 or fp32; out_dtype=float32 is allowed for the
-    residual epilogues (the block keeps its residual stream in fp32)."""
+    residual epilogues (the block keeps its residual stream in fp32).
+    Weights may be float8_e4m3fn with per-output-column fp32 w_scale (one
+    tensor or a list matching the weights): y = acc * w_scale + b."""
     single = torch.is_tensor(weights)
     ws = [weights] if single else list(weights)
     bs = [biases] if (single or biases is None) else list(biases)
     if biases is None:
         bs = [None] * len(ws)
     _req(1 <= len(ws) <= 3 and len(bs) == len(ws), "1 to 3 weight segments")
-    dev = _dev(x, *ws, *[b for b in bs if b is not None], residual)
+    f8 = ws[0].dtype == FP8
+    scs = []
+    if f8:
+        _req(w_scale is not None, "fp8 weights need w_scale")
+        scs = [w_scale] if torch.is_tensor(w_scale) else list(w_scale)
+        _req(len(scs) == len(ws), "one w_scale per weight")
+    else:
+        _req(w_scale is None, "w_scale is only for fp8 weights")
+    dev = _dev(x, *ws, *[b for b in bs if b is not None], residual, *scs)
     _bf16(x, "x")
     _req(x.dim() >= 2 and x.stride(-1) == 1, "x must have a contiguous last dim")
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     M = x2.shape[0]
     N = ws[0].shape[0]
-    for w, b in zip(ws, bs):
-        _bf16(w, "weight")
+    for i, (w, b) in enumerate(zip(ws, bs)):
+        if f8:
+            _req(w.dtype == FP8, "all weights must share one dtype")
+            _req(scs[i].dtype == torch.float32 and scs[i].is_contiguous() and scs[i].numel() == N,
+                 "w_scale must be [N] fp32")
+        else:
+            _bf16(w, "weight")
         _req(w.is_contiguous() and w.shape == (N, K), f"weight must be [{N}, {K}] contiguous")
         if b is not None:
             _bf16(b, "bias")
@@ -111,6 +145,10 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         a.out[i] = o.data_ptr()
     a.ldo = N
     a.epilogue = epilogue
+    if f8:
+        a.w_dtype = _lib.WAM_FP8
+        for i, sc in enumerate(scs):
+            a.w_scale[i] = sc.data_ptr()
     a.out_dtype = dtype_code(outs[0])
     if epilogue in (EPI_BIAS_GATE_RES, EPI_BIAS_RES):
         _req(residual is not None, "residual required")
