@@ -262,6 +262,26 @@ def main():
                      "kernel_us": round(ffn1 * 1e3, 1)},
         "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
     }
+    # C3 second variant: the same layer with e4m3 FFN weights (per-output-channel
+    # fp32 scales, bf16 activations); everything else unchanged.
+    flayer = WholeLayerBlock(blk, ffn_fp8=True)
+    with torch.no_grad():
+        flayer.prepare_context(ctx, precompute=True)
+
+    def fstep(timer=None):
+        with torch.no_grad():
+            return flayer(x, ctx, temb, freqs, timer=timer)
+    fms = timed_steps(fstep, args.steps, args.warmup)
+    fst = stage_times(lib, fstep, 3, (1 << len(_lib.STAGES)) - 1)
+    ffn_flops = 2 * 2 * M * D * F
+    out["fp8_ffn_variant"] = {
+        "us_per_layer": round(fms * 1e3, 1), "tokens_per_s": round(M / (fms * 1e-3), 1),
+        "ffn_unit_us": round((fst["ffn1"] + fst["ffn2"]) * 1e3, 1),
+        "ffn_unit_us_bf16": round((stages["ffn1"] + stages["ffn2"]) * 1e3, 1),
+        "ffn_unit_tflops": round(ffn_flops / ((fst["ffn1"] + fst["ffn2"]) * 1e-3) / 1e12, 1),
+        "weights": "e4m3 per-output-channel scales (absmax/448), bf16 activations, fp32 accumulate",
+    }
+    del flayer
     if not args.no_verify:
         # Lverify: 4 candidates x 1560 tokens, each over the shared 6240-token
         # prefix (pool row 0) plus its own 1560 tokens; read-only cache.

@@ -217,6 +217,12 @@ typedef struct {
   int table_dtype; int norm2_dtype;
   int dim, heads, head_dim, ffn_dim;
   float eps[7];
+  /* Optional fp8 FFN (no counterpart in the reference): when ffn_fp8[0] is
+   * set, FFN1 uses e4m3 weights ffn_fp8[0] [ffn_dim, dim] with per-row scales
+   * ffn_scale[0], and FFN2 ffn_fp8[1] [dim, ffn_dim] with ffn_scale[1]
+   * (wam_quantize_fp8_rows of w[23] and w[25]); the biases stay w[24], w[26]. */
+  const void* ffn_fp8[2];
+  const float* ffn_scale[2];
 } wam_block_weights;
 
 #define WAM_DEBUG_SLOTS 16

@@ -105,3 +105,34 @@ def test_fp8_ffn_unit_vs_fp32(dev):
     m2 = assert_close(y, ref, 0.25, 0.9999, "fp8 FFN vs bf16-weight fp32")
     assert m2["rel_l2"] <= 2e-2, m2
     print("fp8 FFN unit", m, m2, compare(y - res, ref - res))
+
+
+def test_block_with_fp8_ffn(dev):
+    """The whole block with the fp8 FFN: against the fp32 oracle fed the
+    dequantized FFN weights at the block bound, and against the bf16-weight
+    oracle at the fp8 bound."""
+    from oracle.block import block_forward
+    from wam_ops import synthetic
+    from wam_ops.block import TransformerBlock
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = synthetic.BlockShape(3072, 24, 14336)
+    params = synthetic.block_params(shape, seed=21)
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4 * 8 * 8, (4, 8, 8), context_len=512, seed=22)
+    blk = TransformerBlock(shape.dim, shape.ffn, shape.heads, cross_attn_norm=True, eps=shape.eps)
+    with torch.no_grad():
+        for name, prm in blk.named_parameters():
+            prm.data = params[name].to(dev)
+    wl = WholeLayerBlock(blk.to(dev), ffn_fp8=True)
+    with torch.no_grad():
+        wl.prepare_context(ctx.to(dev), precompute=True)
+        out = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+    torch.cuda.synchronize()
+    q1, s1, q2, s2 = wl.bound().ffn_fp8
+    pq = dict(params)
+    pq["ffn.net.0.proj.weight"] = ofp8.dequantize_rows(q1.cpu(), s1.cpu())
+    pq["ffn.net.2.weight"] = ofp8.dequantize_rows(q2.cpu(), s2.cpu())
+    ref_q = block_forward(pq, x, ctx, temb, freqs, shape.heads, shape.eps)
+    assert_close(out.cpu(), ref_q, 2e-2, 0.9999, "block fp8 FFN vs dequantized oracle")
+    ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
+    m = assert_close(out.cpu(), ref, 0.25, 0.9999, "block fp8 FFN vs bf16-weight oracle")
+    print("block fp8 FFN", m)

@@ -121,6 +121,8 @@ static int check_weights(const wam_block_weights* w) {
   WAM_REQUIRE((w->w[1] == nullptr) == (w->w[2] == nullptr), "block: norm2 weight/bias must both be set or both empty");
   WAM_REQUIRE(w->table_dtype == WAM_F32 || w->table_dtype == WAM_BF16, "block: table dtype");
   WAM_REQUIRE(w->norm2_dtype == WAM_F32 || w->norm2_dtype == WAM_BF16, "block: norm2 dtype");
+  WAM_REQUIRE(!w->ffn_fp8[0] || (w->ffn_fp8[1] && w->ffn_scale[0] && w->ffn_scale[1]),
+              "block: fp8 FFN needs both weights and both scale vectors");
   return WAM_OK;
 }
 
@@ -355,6 +357,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     wam_linear_args g;
     gemm_args(g, h, D, R, D, F, W->w[23], W->w[24], act, F);
     g.epilogue = WAM_EPI_BIAS_GELU;
+    if (W->ffn_fp8[0]) {
+      g.w[0] = W->ffn_fp8[0]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[0];
+    }
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 13, act, (size_t)R * F * 2, s));
@@ -364,6 +369,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     wam_linear_args g;
     gemm_args(g, act, F, R, F, D, W->w[25], W->w[26], a->out, D);
     g.epilogue = WAM_EPI_BIAS_GATE_RES; g.res = x2; g.ldr = D; g.res_dtype = WAM_F32;
+    if (W->ffn_fp8[0]) {
+      g.w[0] = W->ffn_fp8[1]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[1];
+    }
     g.gate = mod; g.gate_index = 5;
     WAM_TRY(linear(&g, s));
   }

@@ -81,7 +81,7 @@ class KvCommitArgs(Structure):
 class BlockWeights(Structure):
     _fields_ = [("w", c_void_p * 27), ("table_dtype", c_int), ("norm2_dtype", c_int),
                 ("dim", c_int), ("heads", c_int), ("head_dim", c_int), ("ffn_dim", c_int),
-                ("eps", c_float * 7)]
+                ("eps", c_float * 7), ("ffn_fp8", c_void_p * 2), ("ffn_scale", c_void_p * 2)]
 
 
 class BlockArgs(Structure):

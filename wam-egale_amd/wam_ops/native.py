@@ -48,7 +48,7 @@ def _check(cond, msg):
 class BoundWeights:
     """Validated parameter pointers packed into a wam_block_weights struct."""
 
-    def __init__(self, weights, eps, heads):
+    def __init__(self, weights, eps, heads, ffn_fp8=False):
         _check(len(weights) == 27 and len(eps) == 7, "native parameter schema: 27 weights, 7 eps")
         dev = weights[3].device
         _check(dev.type == "cuda", "native block parameters must live on the GPU")
@@ -67,6 +67,16 @@ class BoundWeights:
         st.dim, st.heads, st.head_dim, st.ffn_dim = dim, heads, dim // heads, self.ffn_dim
         for i, e in enumerate(eps):
             st.eps[i] = float(e)
+        self.ffn_fp8 = None
+        if ffn_fp8:
+            # e4m3 FFN weights with per-output-channel scales (no counterpart in
+            # the reference; the biases stay bf16)
+            from .ops import quantize_fp8_rows
+            q1, s1 = quantize_fp8_rows(weights[23])
+            q2, s2 = quantize_fp8_rows(weights[25])
+            self.ffn_fp8 = (q1, s1, q2, s2)
+            st.ffn_fp8[0], st.ffn_fp8[1] = q1.data_ptr(), q2.data_ptr()
+            st.ffn_scale[0], st.ffn_scale[1] = s1.data_ptr(), s2.data_ptr()
         self.struct = st
 
 

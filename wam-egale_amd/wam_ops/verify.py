@@ -20,8 +20,9 @@ from .whole_layer import WholeLayerBlock
 
 
 class BlockStack:
-    def __init__(self, blocks):
-        self.layers = [b if isinstance(b, WholeLayerBlock) else WholeLayerBlock(b) for b in blocks]
+    def __init__(self, blocks, ffn_fp8=False):
+        self.layers = [b if isinstance(b, WholeLayerBlock) else WholeLayerBlock(b, ffn_fp8=ffn_fp8)
+                       for b in blocks]
         if not self.layers:
             raise ValueError("BlockStack needs at least one block")
         self._ws = None
