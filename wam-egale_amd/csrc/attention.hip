@@ -43,9 +43,14 @@ __device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n -
 
 // Workgroup: W waves x 32 queries of one (batch row, head).  Wave w owns
 // queries q0 + 32 w .. +32 and keeps its Q fragments in registers.
+// n_split > 1: the key tiles of each (query tile, batch row, head) are split
+// into n_split contiguous ranges, one per workgroup; each writes its
+// unnormalised O and its (max, sum) to `part`, and attention_combine_kernel
+// merges them.  Used when the query grid alone would leave CUs idle.
 template <int W>
 __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args a,
-                                                              const int* __restrict__ slots) {
+                                                              const int* __restrict__ slots,
+                                                              int n_split, float* __restrict__ part) {
   // One __shared__ object per stage: the compiler tracks direct-to-LDS loads
   // per object, so reading one stage while others are being filled does not
   // wait for those loads.
@@ -63,7 +68,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 
   const int nqt = (a.Mq + QT - 1) / QT;
   const int id = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
-  const int qt = id % nqt, bh = id / nqt;
+  const int qt = id % nqt, rest = id / nqt;
+  const int split = rest % n_split, bh = rest / n_split;
   const int h = bh % a.H, b = bh / a.H;
 
   const int n_hist = a.n_hist_dev ? __builtin_amdgcn_readfirstlane(*a.n_hist_dev) : 0;
@@ -130,10 +136,14 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   // d = 32 dt + 16 ((lane / 16) % 2) + 4 (lane % 4).
   const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
 
-  const int ntiles = (n_tot + kAttnKT - 1) / kAttnKT;
+  // Key tiles [t_first, t_first + ntiles) of this workgroup's split; t below
+  // counts from t_first.
+  const int all_tiles = (n_tot + kAttnKT - 1) / kAttnKT;
+  const int t_first = (int)((int64_t)split * all_tiles / n_split);
+  const int ntiles = (int)((int64_t)(split + 1) * all_tiles / n_split) - t_first;
 #pragma unroll
   for (int st = 0; st < kAttnStages - 1; ++st)
-    if (st < ntiles) issue(st, WAM_ATTN_BUF(st));
+    if (st < ntiles) issue(t_first + st, WAM_ATTN_BUF(st));
 
   // The tile loop is unrolled by the stage count so that every LDS reference
   // is to a fixed __shared__ object.
@@ -150,7 +160,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
       }
       __builtin_amdgcn_s_barrier();
-      if (t + kAttnStages - 1 < ntiles) issue(t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages));
+      if (t + kAttnStages - 1 < ntiles)
+        issue(t_first + t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages));
       const char* kb = WAM_ATTN_BUF(st);
       const char* vb = kb + kAttnTile;
 
@@ -164,12 +175,12 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
           s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(key, 2 * ks + half)), qf[ks],
                                                           s[kt], 0, 0, 0);
       }
-      if ((t + 1) * kAttnKT > n_tot) {
+      if ((t_first + t + 1) * kAttnKT > n_tot) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int j = t * kAttnKT + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            const int j = (t_first + t) * kAttnKT + kt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
             if (j >= n_tot) s[kt][v] = -INFINITY;
           }
       }
@@ -230,6 +241,25 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 #undef WAM_ATTN_BUF
 
   const float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (n_split > 1) {
+    // Partial result of this split: O (unnormalised, relative to m_run), and
+    // (m_run, l) of the query; an empty split leaves m = -inf, l = 0, O = 0.
+    if (q_ok) {
+      const int64_t row = (((int64_t)split * a.B + b) * a.Mq + qi) * a.H + h;
+      float* op = part + row * kAttnHD;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(op + dt * 32 + 8 * g + 4 * half) =
+              make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+      if (half == 0) {
+        float* ml = part + (int64_t)n_split * a.B * a.Mq * a.H * kAttnHD + row * 2;
+        *reinterpret_cast<float2*>(ml) = make_float2(m_run, l);
+      }
+    }
+    return;
+  }
   const float inv = 1.f / l;
   if (q_ok) {
     bf16* op = static_cast<bf16*>(a.o) + (int64_t)b * a.o_bstride + (int64_t)qi * a.o_rstride + h * kAttnHD;
@@ -243,6 +273,52 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
         *reinterpret_cast<bf16x4*>(op + dt * 32 + 8 * g + 4 * half) = t4;
       }
   }
+}
+
+// Merge the n_split partial results of one (batch row, query, head) row:
+// O = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with m = max_i m_i.  One
+// wave per row, two of the 128 outputs per lane.
+__global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_args a, int n_split,
+                                                                const float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = (int64_t)a.B * a.Mq * a.H;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* ml = part + (int64_t)n_split * rows * kAttnHD;
+  float m = -INFINITY;
+  for (int i = 0; i < n_split; ++i) m = fmaxf(m, ml[((int64_t)i * rows + row) * 2]);
+  float den = 0.f, n0 = 0.f, n1 = 0.f;
+  for (int i = 0; i < n_split; ++i) {
+    const float mi = ml[((int64_t)i * rows + row) * 2];
+    const float w = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - m);
+    den += w * ml[((int64_t)i * rows + row) * 2 + 1];
+    const float2 v = *reinterpret_cast<const float2*>(part + ((int64_t)i * rows + row) * kAttnHD + 2 * lane);
+    n0 += w * v.x;
+    n1 += w * v.y;
+  }
+  const int h = (int)(row % a.H);
+  const int64_t bq = row / a.H;
+  const int qi = (int)(bq % a.Mq), b = (int)(bq / a.Mq);
+  bf16* op = static_cast<bf16*>(a.o) + (int64_t)b * a.o_bstride + (int64_t)qi * a.o_rstride + h * kAttnHD;
+  const float inv = 1.f / den;
+  bf16x2 r;
+  r[0] = static_cast<bf16>(n0 * inv);
+  r[1] = static_cast<bf16>(n1 * inv);
+  *reinterpret_cast<bf16x2*>(op + 2 * lane) = r;
+}
+
+// Key-range splits for a query grid of `base` 256-query workgroups: enough to
+// give every CU about two workgroups, at most 8.
+static int attention_splits(int B, int Mq, int H) {
+  const int64_t base = (int64_t)((Mq + 255) / 256) * H * B;
+  if (base >= 384 || base <= 0) return 1;
+  const int64_t ns = (512 + base - 1) / base;
+  return (int)(ns < 8 ? ns : 8);
+}
+
+int64_t attention_workspace_bytes(int B, int Mq, int H) {
+  const int ns = attention_splits(B, Mq, H);
+  return ns > 1 ? (int64_t)ns * B * Mq * H * (kAttnHD + 2) * 4 : 0;
 }
 
 int attention(const wam_attention_args* a, hipStream_t s) {
@@ -269,14 +345,28 @@ int attention(const wam_attention_args* a, hipStream_t s) {
     WAM_REQUIRE(a->B <= a->kv_batch || a->kv_batch == 1,
                 "wam_attention: B=%d exceeds kv batch %d", a->B, a->kv_batch);
   if (a->Mq == 0) return WAM_OK;
-  // 8 waves (256 queries) per workgroup when that still fills the chip.
+  // 8 waves (256 queries) per workgroup when that still fills the chip;
+  // otherwise key-range splits (when the caller gave a workspace for the
+  // partial results), else 4-wave workgroups.
   const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
+  WAM_REQUIRE(grid8 < (1 << 26), "wam_attention: grid too large");
+  const int ns = attention_splits(a->B, a->Mq, a->H);
+  if (ns > 1 && a->workspace && a->workspace_bytes >= attention_workspace_bytes(a->B, a->Mq, a->H)) {
+    float* part = static_cast<float*>(a->workspace);
+    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)(grid8 * ns)), dim3(512), 0, s, *a, a->slots, ns,
+                       part);
+    WAM_LAUNCHED("attention_kernel");
+    const int64_t rows = (int64_t)a->B * a->Mq * a->H;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, *a, ns,
+                       static_cast<const float*>(part));
+    WAM_LAUNCHED("attention_combine_kernel");
+    return WAM_OK;
+  }
   if (grid8 >= 256) {
-    WAM_REQUIRE(grid8 < (1 << 30), "wam_attention: grid too large");
-    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots);
+    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, 1, nullptr);
   } else {
     const int64_t grid4 = (int64_t)((a->Mq + 127) / 128) * a->H * a->B;
-    hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid4), dim3(256), 0, s, *a, a->slots);
+    hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid4), dim3(256), 0, s, *a, a->slots, 1, nullptr);
   }
   WAM_LAUNCHED("attention_kernel");
   return WAM_OK;
@@ -286,4 +376,8 @@ int attention(const wam_attention_args* a, hipStream_t s) {
 
 extern "C" int wam_attention(const wam_attention_args* args, void* stream) {
   return wam::attention(args, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t wam_attention_workspace_bytes(int B, int Mq, int H) {
+  return wam::attention_workspace_bytes(B, Mq, H);
 }

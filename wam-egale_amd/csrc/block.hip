@@ -30,6 +30,7 @@ int linear(const wam_linear_args*, hipStream_t);
 int ln_modulate(const wam_ln_args*, hipStream_t);
 int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
+int64_t attention_workspace_bytes(int B, int Mq, int H);
 int kv_layout(const wam_kv_layout_args*, hipStream_t);
 int kv_commit(const wam_kv_commit_args*, hipStream_t);
 
@@ -68,7 +69,7 @@ struct Scope {
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct Layout {
-  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, total;
+  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, attnws, attnws_bytes, total;
 };
 
 static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
@@ -87,6 +88,9 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   L.slots = take((size_t)(pool > 0 ? pool : 1) * 4);
   L.newslots = take((size_t)(M > 0 ? M : 1) * 4);
   L.info = take(16);
+  // key-range split partials of the self and cross attention (same query grid)
+  L.attnws_bytes = (size_t)attention_workspace_bytes(B, M, D / 128);
+  L.attnws = take(L.attnws_bytes);
   L.total = off;
   return L;
 }
@@ -255,6 +259,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.k = qkv + D; t.v = qkv + 2 * D; t.kv_bstride = (int64_t)M * 3 * D; t.kv_rstride = 3 * D;
     t.Mk = M; t.kv_batch = B;
     t.scale = 1.0f / sqrtf((float)W->head_dim);
+    t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
     WAM_TRY(attention(&t, s));
   }
   WAM_TRY(copy_debug(a->debug, 4, attn, rowb, s));
@@ -329,6 +334,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.Mk = a->context_len; t.kv_batch = a->context_batch;
     t.kv_rows = a->context_rows;
     t.scale = 1.0f / sqrtf((float)W->head_dim);
+    t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
     WAM_TRY(attention(&t, s));
   }
   WAM_TRY(copy_debug(a->debug, 10, attn, rowb, s));

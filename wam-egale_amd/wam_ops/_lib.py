@@ -62,7 +62,8 @@ class AttentionArgs(Structure):
                 ("pool_rstride", c_int64), ("pool_batch", c_int), ("slots", c_void_p),
                 ("n_hist_dev", c_void_p), ("pool_rows", c_void_p), ("k", c_void_p),
                 ("v", c_void_p), ("kv_bstride", c_int64), ("kv_rstride", c_int64),
-                ("Mk", c_int), ("kv_rows", c_void_p), ("kv_batch", c_int), ("scale", c_float)]
+                ("Mk", c_int), ("kv_rows", c_void_p), ("kv_batch", c_int), ("scale", c_float),
+                ("workspace", c_void_p), ("workspace_bytes", c_int64)]
 
 
 class KvLayoutArgs(Structure):
@@ -106,6 +107,7 @@ STRUCTS = {
 # Every symbol include/wam_block.h declares, with its ctypes signature.
 SIGNATURES = {
     "wam_linear": (c_int, [POINTER(LinearArgs), c_void_p]),
+    "wam_attention_workspace_bytes": (c_int64, [c_int, c_int, c_int]),
     "wam_quantize_fp8_rows": (c_int, [c_void_p, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
     "wam_ln_modulate": (c_int, [POINTER(LnArgs), c_void_p]),
     "wam_rms_rope": (c_int, [POINTER(RmsRopeArgs), c_void_p]),
