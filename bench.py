@@ -158,6 +158,30 @@ def measured_traffic():
     return None
 
 
+def _unit(ms, flop):
+    return {"us": round(ms * 1e3, 1), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+            "frac_of_bf16_peak": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
+def c4a_attention(shape, dev, steps, warmup, q_tokens=1560, prefix=6240):
+    """Self attention of 1560 new tokens over a 6240-token cached prefix (pool
+    row 0 through the slot list) plus themselves, 24 x 128 heads; N(0, 1) Q/K/V."""
+    import torch
+    from wam_ops import ops
+    H = shape.heads
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(1, q_tokens, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(1, q_tokens, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(1, q_tokens, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    pk = torch.randn(1, prefix, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    pv = torch.randn(1, prefix, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    slots = torch.arange(prefix, dtype=torch.int32, device=dev)
+    n_hist = torch.tensor([prefix], dtype=torch.int32, device=dev)
+    ms = timed_steps(lambda: ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n_hist),
+                     steps, warmup)
+    return _unit(ms, 4 * q_tokens * (prefix + q_tokens) * shape.dim)
+
+
 def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup, layers=30):
     """C5: the 30-layer speculative verify forward (BlockStack) measured as a
     whole: 30 random-init layers, each with its own 6240-token committed prefix
@@ -261,6 +285,17 @@ def main():
                      "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(ffn1 * 1e3, 1)},
         "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
+    }
+    # Per-unit lines of the same run (algorithmic FLOP as in the layer count):
+    # C2 QKV + q/k RMSNorm + RoPE, C3 FFN (FFN1 + GELU + FFN2 + gated
+    # residual), C4b cross attention over 512 keys, from the stage timers of
+    # the layer; C4a self attention (1560 queries over a 6240-token cached
+    # prefix + themselves) as its own call.
+    out["units"] = {
+        "C2_qkv_rms_rope": _unit(stages["qkv"] + stages["rms_rope"], 2 * M * D * 3 * D),
+        "C3_ffn": _unit(stages["ffn1"] + stages["ffn2"], 2 * 2 * M * D * F),
+        "C4b_cross_attention": _unit(stages["cross_attn"], 4 * M * Lc * D),
+        "C4a_self_attention": c4a_attention(shape, dev, args.steps, args.warmup),
     }
     # C3 second variant: the same layer with e4m3 FFN weights (per-output-channel
     # fp32 scales, bf16 activations); everything else unchanged.

@@ -165,16 +165,17 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
       const char* kb = WAM_ATTN_BUF(st);
       const char* vb = kb + kAttnTile;
 
+      // The two 32-key halves alternate, so consecutive MFMAs never wait on
+      // each other's accumulator.
       f32x16 s[2];
+      s[0] = f32x16{};
+      s[1] = f32x16{};
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = f32x16{};
-        const int key = kt * 32 + l32;
+      for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(key, 2 * ks + half)), qf[ks],
-                                                          s[kt], 0, 0, 0);
-      }
+        for (int kt = 0; kt < 2; ++kt)
+          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(kt * 32 + l32, 2 * ks + half)),
+                                                          qf[ks], s[kt], 0, 0, 0);
       if ((t_first + t + 1) * kAttnKT > n_tot) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)

@@ -78,7 +78,8 @@ __device__ inline int lds_off(int r, int c) {
 
 __device__ inline void ld_mod4(const wam_modulation m, int D, int64_t row, int idx,
                                int d, float out[4]) {
-  const int64_t b = row / m.tokens, t = row - b * m.tokens;
+  int64_t b, t;
+  split_row(row, m.tokens, b, t);
   const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
   const int64_t toff = (trow * 6 + idx) * (int64_t)D + d;
   const int64_t tab = (int64_t)idx * D + d;

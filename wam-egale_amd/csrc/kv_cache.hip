@@ -181,9 +181,11 @@ __global__ __launch_bounds__(256) void kv_commit_kernel(wam_kv_commit_args a) {
   const int chunks = a.D >> 3;
   const int64_t n = (int64_t)a.B * a.tokens * chunks;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    const int64_t row = i / chunks;
-    const int c = (int)(i - row * chunks);
-    const int64_t b = row / a.tokens, t = row - b * a.tokens;
+    int64_t row, cc;
+    split_row(i, chunks, row, cc);  // i < 2^31: B * tokens * D / 8 elements
+    const int c = (int)cc;
+    int64_t b, t;
+    split_row(row, a.tokens, b, t);
     const int64_t src = row * a.ld + c * 8;
     const int64_t dst = b * a.pool_bstride + (int64_t)a.new_slots[t] * a.pool_rstride + c * 8;
     st_bf16x8(static_cast<bf16*>(a.pool_k) + dst, ld_bf16x8(static_cast<const bf16*>(a.k) + src));
@@ -197,6 +199,7 @@ int kv_commit(const wam_kv_commit_args* a, hipStream_t s) {
   WAM_REQUIRE(a->D % 8 == 0 && a->ld % 8 == 0 && a->pool_rstride % 8 == 0 && a->pool_bstride % 8 == 0,
               "wam_kv_commit: 16-byte alignment contract");
   const int64_t n = (int64_t)a->B * a->tokens * (a->D / 8);
+  WAM_REQUIRE(a->B >= 0 && a->tokens >= 0 && n < (1ll << 31), "wam_kv_commit: B * tokens * D / 8 must be < 2^31");
   if (n == 0) return WAM_OK;
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(kv_commit_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, *a);

@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256) void rms_rope_kernel(wam_rms_rope_args a) {
   const float rstd = rsqrtf(wave_sum(q) / D + eps);
   const float2* f = nullptr;
   if (a.freq) {
-    const int64_t b = row / a.tokens, t = row - b * a.tokens;
+    int64_t b, t;
+    split_row(row, a.tokens, b, t);
     const int64_t fb = a.freq_batch == 1 ? 0 : b;
     f = static_cast<const float2*>(a.freq) + (fb * a.tokens + t) * (a.head_dim / 2);
   }

@@ -162,6 +162,16 @@ __device__ inline void st_bf16x8(void* p, bf16x8 v) {
   *reinterpret_cast<bf16x8*>(p) = v;
 }
 
+// (b, t) = (row / tokens, row % tokens) in 32-bit arithmetic (token rows are
+// below 2^31 everywhere in this library; a 64-bit division is a long
+// software sequence on the GPU).
+__device__ inline void split_row(int64_t row, int tokens, int64_t& b, int64_t& t) {
+  const uint32_t r = (uint32_t)row, n = (uint32_t)tokens;
+  const uint32_t q = r / n;
+  b = q;
+  t = r - q * n;
+}
+
 // 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb,
 // for token row `row` (b = row / tokens, t = row % tokens).
 __device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[8]) {
@@ -177,7 +187,8 @@ __device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[
   }
 }
 __device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx, int d, float out[8]) {
-  const int64_t b = row / m.tokens, t = row - b * m.tokens;
+  int64_t b, t;
+  split_row(row, m.tokens, b, t);
   const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
   float tb[8];
   ld8_f32(m.table, m.table_dtype, (int64_t)idx * D + d, out);
