@@ -34,10 +34,14 @@ struct LinearParams {
 };
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0,
-          int WB_ = 2>
+          int WB_ = 2, int SPLIT_ = 1>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
   static constexpr int WB = WB_;          // bytes per weight element: 2 (bf16) or 1 (fp8 e4m3)
+  // SPLIT > 1: a stage's loads are issued in SPLIT parts, one at the barrier
+  // and the others before the MFMAs of the next k-step's first sub-steps, so
+  // the load issue does not stall the waves all at once (needs STAGES >= 3).
+  static constexpr int SPLIT = SPLIT_;
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
   static constexpr int SCHED = SCHED_;    // 1: alternate DS reads and MFMAs; 2: all reads of
                                           // the next k-step, then this step's MFMAs
@@ -62,6 +66,8 @@ struct GemmCfg {
                 "loads per wave: A then W");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(STAGES >= 2 && BLOCKS * (STAGES * STAGE + (5 - STAGES) * 1024) <= 160 * 1024, "LDS budget");
+  static_assert(SPLIT == 1 || (STAGES >= 3 && LOADS_PER_WAVE % SPLIT == 0 && SPLIT - 1 <= BK / 16 - 1),
+                "split load issue");
 };
 
 // Byte offset of logical 16-byte chunk `c` of LDS row `r`.  The gfx950 LDS
@@ -115,13 +121,15 @@ __device__ inline void wait_vmcnt() {
 // g = w + i * kWaves; whether a load reads A or W depends on i only, so the
 // unrolled sequence has no branches.  a_lane / b_lane already include the
 // swizzle term of the wave's block parity (the wave count is even).
-template <class C>
+template <class C, int NPARTS = 1>
 __device__ __forceinline__ void issue_stage(char* base, i32x4 ra, i32x4 rb, int wave, int a_lane,
-                                            int b_lane, int a_pitch, int b_pitch, int kt) {
+                                            int b_lane, int a_pitch, int b_pitch, int kt, int part = 0) {
   const int ko = kt * C::BK * 2, ko_w = kt * C::BK * C::WB;
   constexpr int A_ITERS = C::A_LOADS / C::kWaves;
+  constexpr int PER = C::LOADS_PER_WAVE / NPARTS;
 #pragma unroll
-  for (int i = 0; i < C::LOADS_PER_WAVE; ++i) {
+  for (int ip = 0; ip < PER; ++ip) {
+    const int i = part * PER + ip;  // part is a constant wherever the caller is unrolled
     const int g = wave + i * C::kWaves;
     char* dst = base + g * 1024;
     if (i < A_ITERS)
@@ -253,6 +261,13 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       // step's MFMAs.
 #pragma unroll
       for (int ks = 0; ks + 1 < KSTEPS; ++ks) {
+        if constexpr (C::SPLIT > 1) {
+          // the remaining parts of the loads issued at the previous barrier
+          // (tile kt - 1 + STAGES into the previous stage's buffer)
+          if (ks + 1 < C::SPLIT && kt >= 1 && kt - 1 + C::STAGES < nk)
+            issue_stage<C, C::SPLIT>(WAM_GEMM_BUF((st + C::STAGES - 1) % C::STAGES), ra, rb, wave, a_lane,
+                                     b_lane, a_pitch, b_pitch, kt - 1 + C::STAGES, ks + 1);
+        }
         fetch_frags<C>(abase, bbase, wm, wn, l32, (ks + 1) * 2 + half, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
         for (int j = 0; j < C::TN; ++j)
@@ -282,7 +297,8 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         if (kt + C::STAGES < nk)
-          issue_stage<C>(WAM_GEMM_BUF(st), ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch, kt + C::STAGES);
+          issue_stage<C, C::SPLIT>(WAM_GEMM_BUF(st), ra, rb, wave, a_lane, b_lane, a_pitch, b_pitch,
+                                   kt + C::STAGES, 0);
         const char* na = WAM_GEMM_BUF((st + 1) % C::STAGES);
         fetch_frags<C>(na, na + C::A_BYTES, wm, wn, l32, half, fa[0], fb[0]);
       }
@@ -406,9 +422,11 @@ using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
 using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
 using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
 using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
-// fp8 e4m3 weights (64-byte LDS weight rows, three stages)
-using Cfg256x256f8 = GemmCfg<256, 256, 64, 2, 4, 3, 1, 2, 1>;
+// fp8 e4m3 weights (64-byte LDS weight rows, three stages, loads issued in
+// three parts)
+using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 3, 1, 2, 1, 3>;
 using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
+using Cfg256x256k32w8t4s2 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2, 2, 2>;
 
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
@@ -446,6 +464,7 @@ static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool
   if (!strcmp(name, "256x256w8t")) return launch_gemm<Cfg256x256w8t>(p, s);
   if (!strcmp(name, "256x256k32w8t4")) return launch_gemm<Cfg256x256k32w8t4>(p, s);
   if (!strcmp(name, "256x128k32w4b2s")) return launch_gemm<Cfg256x128k32w4b2s>(p, s);
+  if (!strcmp(name, "256x256k32w8t4s2")) return launch_gemm<Cfg256x256k32w8t4s2>(p, s);
   *found = false;
   return WAM_OK;
 }
@@ -547,7 +566,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.n_off = 0;
   const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
   if (f8) {
-    if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256f8, Cfg128x128f8>(p, s);
+    if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, s);
     return launch_gemm<Cfg128x128f8>(p, s);
   }
   const char* force = getenv("WAM_GEMM_CFG");
