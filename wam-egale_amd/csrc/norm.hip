@@ -17,10 +17,13 @@
 namespace wam {
 
 // ------------------------------------------------------------- LayerNorm
-// Each wave normalises kRowsPerWave consecutive rows, loading row r+1 while
-// it reduces row r; the modulation (or affine) vectors are loaded once and
-// reused while consecutive rows share a sample.
-constexpr int kRowsPerWave = 1;
+// One wave per row, 8 rows per workgroup.  The per-column vectors the rows
+// multiply and add (1 + scale and shift of the modulation, or gamma and beta)
+// are the same for every row of a sample: when the workgroup's rows share
+// them, they are formed once into LDS (fp32) and every wave reads them there.
+// Loaded per wave instead, they were 8x the bytes of the bf16 row itself.
+constexpr int kLnWaves = 8;
+constexpr int kLnMaxD = 4096;
 
 template <int CH, bool XF32>
 __device__ inline void ln_load_row(const void* x, int64_t row, int D, int lane, float v[CH][8]) {
@@ -37,78 +40,93 @@ __device__ inline void ln_load_row(const void* x, int64_t row, int D, int lane, 
   }
 }
 
+// mul/add of 8 columns at ch*8 for token row `row`, from global memory.
+__device__ inline void ln_coeffs(const wam_ln_args& a, int64_t row, int ch, float mul[8], float add[8]) {
+  if (a.affine) {
+    ld8_f32(a.gamma, a.gb_dtype, ch * 8, mul);
+    ld8_f32(a.beta, a.gb_dtype, ch * 8, add);
+  } else {
+    ld_mod8(a.mod, a.D, row, a.shift_index, ch * 8, add);
+    ld_mod8(a.mod, a.D, row, a.shift_index + 1, ch * 8, mul);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mul[e] += 1.f;
+  }
+}
+
 template <int CH, bool XF32>
-__global__ __launch_bounds__(256) void ln_modulate_kernel(wam_ln_args a) {
+__global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args a) {
+  __shared__ __attribute__((aligned(16))) float s_mul[kLnMaxD];
+  __shared__ __attribute__((aligned(16))) float s_add[kLnMaxD];
   const int lane = threadIdx.x & 63;
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
-  if (row0 >= a.rows) return;
+  const int64_t first = (int64_t)blockIdx.x * kLnWaves;
+  const int64_t last = min(first + kLnWaves, (int64_t)a.rows) - 1;
+  const int64_t row = first + (threadIdx.x >> 6);
   const int D = a.D, nch = D >> 3;
-  float mul[CH][8], add[CH][8];
-  int64_t mod_key = -1;  // sample (or token row) whose modulation is loaded
-  float v[CH][8], nxt[CH][8];
-  ln_load_row<CH, XF32>(a.x, row0, D, lane, v);
-#pragma unroll
-  for (int r = 0; r < kRowsPerWave; ++r) {
-    const int64_t row = row0 + r;
-    if (row >= a.rows) break;
-    if (r + 1 < kRowsPerWave && row + 1 < a.rows) ln_load_row<CH, XF32>(a.x, row + 1, D, lane, nxt);
-    const int64_t key = a.affine ? 0
-                      : (a.mod.temb_len == 1 ? row / a.mod.tokens : row);
-    if (key != mod_key) {
-      mod_key = key;
-#pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int ch = lane + c * 64;
-        if (ch >= nch) continue;
-        if (a.affine) {
-          ld8_f32(a.gamma, a.gb_dtype, ch * 8, mul[c]);
-          ld8_f32(a.beta, a.gb_dtype, ch * 8, add[c]);
-        } else {
-          ld_mod8(a.mod, D, row, a.shift_index, ch * 8, add[c]);
-          ld_mod8(a.mod, D, row, a.shift_index + 1, ch * 8, mul[c]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) mul[c][e] += 1.f;
-        }
-      }
+  // Do all rows of this workgroup use the same coefficients?
+  bool shared = a.affine != 0;
+  if (!shared && a.mod.temb_len == 1) {
+    int64_t b0, b1, t0, t1;
+    split_row(first, a.mod.tokens, b0, t0);
+    split_row(last, a.mod.tokens, b1, t1);
+    shared = b0 == b1;
+  }
+  if (shared) {
+    for (int ch = threadIdx.x; ch < nch; ch += 64 * kLnWaves) {
+      float mul[8], add[8];
+      ln_coeffs(a, first, ch, mul, add);
+      *reinterpret_cast<float4*>(s_mul + ch * 8) = make_float4(mul[0], mul[1], mul[2], mul[3]);
+      *reinterpret_cast<float4*>(s_mul + ch * 8 + 4) = make_float4(mul[4], mul[5], mul[6], mul[7]);
+      *reinterpret_cast<float4*>(s_add + ch * 8) = make_float4(add[0], add[1], add[2], add[3]);
+      *reinterpret_cast<float4*>(s_add + ch * 8 + 4) = make_float4(add[4], add[5], add[6], add[7]);
     }
-    float s = 0.f;
+    __syncthreads();
+  }
+  if (row >= a.rows) return;
+  float v[CH][8];
+  ln_load_row<CH, XF32>(a.x, row, D, lane, v);
+  float s = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+  for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s += v[c][e];
-    const float mean = wave_sum(s) / D;
-    float q = 0.f;
+    for (int e = 0; e < 8; ++e) s += v[c][e];
+  const float mean = wave_sum(s) / D;
+  float q = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (lane + c * 64 < nch) {
+  for (int c = 0; c < CH; ++c) {
+    if (lane + c * 64 < nch) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { const float d = v[c][e] - mean; q += d * d; }
-      }
+      for (int e = 0; e < 8; ++e) { const float d = v[c][e] - mean; q += d * d; }
     }
-    const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
-    bf16* y = static_cast<bf16*>(a.y) + row * D;
+  }
+  const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
+  bf16* y = static_cast<bf16*>(a.y) + row * D;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const int ch = lane + c * 64;
-      if (ch >= nch) continue;
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[c][e] + add[c][e]);
-      st_bf16x8(y + ch * 8, o);
+  for (int c = 0; c < CH; ++c) {
+    const int ch = lane + c * 64;
+    if (ch >= nch) continue;
+    float mul[8], add[8];
+    if (shared) {
+      const float4 m0 = *reinterpret_cast<const float4*>(s_mul + ch * 8);
+      const float4 m1 = *reinterpret_cast<const float4*>(s_mul + ch * 8 + 4);
+      const float4 a0 = *reinterpret_cast<const float4*>(s_add + ch * 8);
+      const float4 a1 = *reinterpret_cast<const float4*>(s_add + ch * 8 + 4);
+      mul[0] = m0.x; mul[1] = m0.y; mul[2] = m0.z; mul[3] = m0.w;
+      mul[4] = m1.x; mul[5] = m1.y; mul[6] = m1.z; mul[7] = m1.w;
+      add[0] = a0.x; add[1] = a0.y; add[2] = a0.z; add[3] = a0.w;
+      add[4] = a1.x; add[5] = a1.y; add[6] = a1.z; add[7] = a1.w;
+    } else {
+      ln_coeffs(a, row, ch, mul, add);
     }
-    if (r + 1 < kRowsPerWave) {
+    bf16x8 o;
 #pragma unroll
-      for (int c = 0; c < CH; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = nxt[c][e];
-    }
+    for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[e] + add[e]);
+    st_bf16x8(y + ch * 8, o);
   }
 }
 
 template <bool XF32>
 static void launch_ln(const wam_ln_args* a, hipStream_t s) {
-  const int64_t waves = (a->rows + kRowsPerWave - 1) / kRowsPerWave;
-  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  const dim3 grid((unsigned)((a->rows + kLnWaves - 1) / kLnWaves)), block(64 * kLnWaves);
   const int ch = (a->D / 8 + 63) / 64;
   if (ch <= 1) hipLaunchKernelGGL((ln_modulate_kernel<1, XF32>), grid, block, 0, s, *a);
   else if (ch <= 2) hipLaunchKernelGGL((ln_modulate_kernel<2, XF32>), grid, block, 0, s, *a);
