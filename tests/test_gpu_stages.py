@@ -32,7 +32,8 @@ def _ref_linear(x, w, b):
 
 
 @pytest.mark.parametrize("M,K,N,nseg", [(1, 64, 128, 1), (300, 256, 384, 1), (77, 512, 256, 3),
-                                        (4680, 3072, 3072, 1), (520, 3072, 3072, 3)])
+                                        (4680, 3072, 3072, 1), (520, 3072, 3072, 3),
+                                        (300, 256, 192, 1), (70, 192, 200, 1), (4680, 3072, 192, 1)])
 def test_linear_bias(dev, M, K, N, nseg):
     from wam_ops import ops
     x = _randn((M, K), dev, 1)

@@ -203,7 +203,9 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // buffer resource and load as zeros.
   const uint32_t a_bytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u;
   const i32x4 ra = make_rsrc4(A + (int64_t)m0 * p.lda, a_bytes);
-  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)C::BN * p.ldw * C::WB));
+  // Weight rows past N (a partial last n-tile) load as zeros.
+  const int n_rows = min(C::BN, p.seg_n - n0);
+  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)n_rows * p.ldw * C::WB));
   const int lrow = lane / C::KCH, pchunk = lane % C::KCH;
   // The swizzle term of row r = ROWS_PER_LOAD * g + lrow: for 128-byte rows
   // (8 rows per block) it depends on the parity of g, for 64-byte rows (16
@@ -331,8 +333,9 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   const bf16* __restrict__ bias = seg == 0 ? p.bias[0] : (seg == 1 ? p.bias[1] : p.bias[2]);
   const int q = lane % QPR;  // this lane's chunk of a row in the read phase
   const int n = n0 + 4 * q;
+  const bool n_ok = n < p.seg_n;  // N is a multiple of 4: a lane's 4 columns are all in or all out
   float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (bias) {
+  if (bias && n_ok) {
     const bf16x4 t = *reinterpret_cast<const bf16x4*>(bias + n);
 #pragma unroll
     for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
@@ -340,7 +343,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   float wsc[4] = {1.f, 1.f, 1.f, 1.f};
   if constexpr (C::WB == 1) {
     const float* ws = seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2]);
-    const float4 t = *reinterpret_cast<const float4*>(ws + n);
+    const float4 t = n_ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
   __syncthreads();  // every wave is done reading the last stage
@@ -368,7 +371,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
       const int row = rd * ROUND + rr;
       const int m = m0 + row;
-      if (row >= C::BM || m >= p.M) continue;
+      if (row >= C::BM || m >= p.M || !n_ok) continue;
       const int obj = rr / RPO, lr = rr % RPO;
       const char* buf = WAM_GEMM_BUF(obj);
       const f32x4 v = *reinterpret_cast<const f32x4*>(buf + lr * ROW_B + ((q ^ (lr & 15)) << 4));
@@ -430,9 +433,9 @@ using Cfg256x256k32w8t4s2 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2, 2, 2>;
 
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
-  WAM_REQUIRE(p.seg_n % C::BN == 0 && p.K % C::BK == 0,
+  WAM_REQUIRE(p.K % C::BK == 0 && (p.n_seg_count == 1 || p.seg_n % C::BN == 0),
               "wam_linear: N=%d / K=%d do not fit a %dx%dx%d tile", p.seg_n, p.K, C::BM, C::BN, C::BK);
-  p.n_tiles_per_seg = p.seg_n / C::BN;
+  p.n_tiles_per_seg = (p.seg_n + C::BN - 1) / C::BN;
   p.m_tiles = (p.M + C::BM - 1) / C::BM;
   p.n_tiles = p.n_tiles_per_seg * p.n_seg_count;
   const int grid = p.m_tiles * p.n_tiles;
@@ -520,7 +523,8 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a->M >= 1 && a->K >= 1 && a->seg_n >= 1, "wam_linear: empty shape M=%d K=%d N=%d",
               a->M, a->K, a->seg_n);
   WAM_REQUIRE(a->K % 64 == 0, "wam_linear: K=%d must be a multiple of 64", a->K);
-  WAM_REQUIRE(a->seg_n % 128 == 0, "wam_linear: N=%d must be a multiple of 128", a->seg_n);
+  WAM_REQUIRE(a->seg_n % 8 == 0 && (a->n_seg == 1 || a->seg_n % 128 == 0),
+              "wam_linear: N=%d must be a multiple of 8 (of 128 with several segments)", a->seg_n);
   WAM_REQUIRE(a->w_dtype == WAM_BF16 || a->w_dtype == WAM_FP8, "wam_linear: w_dtype %d", a->w_dtype);
   const bool f8 = a->w_dtype == WAM_FP8;
   const int wb = f8 ? 1 : 2;
