@@ -40,6 +40,18 @@
  *   wam_kv_layout          <- layout_kernel (slot compaction, eviction, new-slot
  *                             bookkeeping) 算子研究/wam_ops/baseline/csrc/block.cu:133-200
  *   wam_kv_commit          <- private_kernel 算子研究/wam_ops/baseline/csrc/block.cu:201-212
+ * Model input/output around the block loop (WanTransformer3DModel.forward,
+ * 投机采样/wam-p0-worktree/wan_va/modules/model.py:1060-1116; the reference
+ * runs these as torch ops, it has no native kernels for them):
+ *   wam_patchify           <- rearrange of the latents before patch_embedding_mlp /
+ *                             action_embedder (model.py:1060-1071)
+ *   wam_timestep_embedding <- condition_embedder.timesteps_proj (diffusers
+ *                             Timesteps, model.py:216-218,233)
+ *   wam_rows_linear        <- time_embedder / time_proj / action_proj_out linears
+ *                             on few rows (model.py:219-222,234-239,1109)
+ *   wam_rope_freqs         <- WanRotaryPosEmbed.forward (model.py:276-286)
+ *   (norm_out + modulation is wam_ln_modulate with a one-vector temb;
+ *    patch_embedding_mlp, text_embedder and proj_out are wam_linear)
  */
 #ifndef WAM_BLOCK_H
 #define WAM_BLOCK_H
@@ -61,7 +73,8 @@ enum {
 };
 
 /* Element types; zero (a memset struct) means bf16. */
-enum { WAM_BF16 = 0, WAM_F32 = 1, WAM_FP8 = 2 /* OCP e4m3 (e4m3fn), weights only */ };
+enum { WAM_BF16 = 0, WAM_F32 = 1, WAM_FP8 = 2 /* OCP e4m3 (e4m3fn), weights only */,
+       WAM_I64 = 3, WAM_F64 = 4 /* grid ids of wam_rope_freqs only */ };
 
 /* Epilogues of wam_linear. */
 enum {
@@ -71,16 +84,23 @@ enum {
   WAM_EPI_BIAS_RES = 3       /* y = bf16(res + (acc + b))                      */
 };
 
-/* Modulation source: mod[b, t, i, :] = table[i, :] + temb[b, t or 0, i, :]
+/* Modulation source: mod[b, t, i, :] = table[i, :] + temb[b, r(t), i, :]
  * (model.py:751-759; i = 0 shift, 1 scale, 2 gate, 3 c_shift, 4 c_scale,
- * 5 c_gate).  temb is [B, L, 6, D] with L == 1 (per sample) or L == tokens. */
+ * 5 c_gate).  temb is [B, L, mods, D].  L == 1 (per sample), L == tokens
+ * (per token, the reference's timestep_proj), or any divisor of tokens: row
+ * r(t) = t / (tokens / L) then serves tokens / L consecutive tokens (one
+ * latent frame: the reference repeats each frame's timestep over the frame's
+ * tokens, model.py:1078-1086, so per-frame rows give the same values).
+ * mods == 6, or mods == 1 for one vector that serves every index i (the
+ * output head: scale_shift_table[2, D] + temb[B, L, D], model.py:1096). */
 typedef struct {
-  const void* table; /* [6, D] */
+  const void* table; /* [6, D] (or [2, D] for the output head) */
   int table_dtype;   /* WAM_F32 | WAM_BF16 */
-  const void* temb;  /* [B, L, 6, D] */
+  const void* temb;  /* [B, L, mods, D] */
   int temb_dtype;    /* WAM_F32 | WAM_BF16 */
-  int temb_len;      /* L: 1 or tokens */
+  int temb_len;      /* L: 1, tokens, or a divisor of tokens */
   int tokens;        /* tokens per batch row (M) */
+  int temb_mods;     /* mods: 6 (0 is read as 6) or 1 */
 } wam_modulation;
 
 /* ---------------------------------------------------------------- linear */
@@ -271,6 +291,79 @@ int wam_block_forward(const wam_block_args* args, void* stream);
  * (attn2 of model.py:777-782), written to k_out/v_out [rows, D]. */
 int wam_prepare_context(const wam_block_weights* weights, const void* context,
                         int rows, void* k_out, void* v_out, void* stream);
+
+/* ------------------------------------------------- model input / output */
+/* Patch rearrange of the latents (model.py:1064-1069, and 1060-1062 with a
+ * 1x1x1 patch for the action latents):
+ *   out[b*L + (f*Hp + h)*Wp + w, (c*p1 + i)*p2*p3 + j*p3 + k]
+ *       = x[b, c, f*p1 + i, h*p2 + j, w*p3 + k]
+ * with L = Fp*Hp*Wp = (F/p1)(H/p2)(W/p3).  x is [B, C, F, H, W] bf16,
+ * contiguous; out is [B*L, k_pad] bf16 and columns C*p1*p2*p3 .. k_pad-1 are
+ * zero, so a following wam_linear runs with K = k_pad (a multiple of 64)
+ * against weights zero-padded to k_pad columns. */
+typedef struct {
+  const void* x;
+  void* out;
+  int B, C, F, H, W;
+  int p1, p2, p3;
+  int k_pad;
+} wam_patchify_args;
+
+int wam_patchify(const wam_patchify_args* args, void* stream);
+
+/* Sinusoidal timestep embedding, diffusers 0.36.0 get_timestep_embedding as
+ * Timesteps(dim, flip_sin_to_cos, downscale_freq_shift) calls it
+ * (model.py:216-218): freq_i = exp(-ln(max_period) * i / (dim/2 - shift)),
+ * fp32, i < dim/2; out[r] = [cos(t_r freq), sin(t_r freq)] when
+ * flip_sin_to_cos, else [sin, cos]. */
+typedef struct {
+  const float* t;   /* [rows] */
+  int rows, dim;    /* dim even */
+  int flip_sin_to_cos;
+  float shift;      /* downscale_freq_shift */
+  float max_period; /* 10000 */
+  void* out;        /* [rows, dim] */
+  int out_dtype;    /* WAM_F32 | WAM_BF16 */
+} wam_timestep_args;
+
+int wam_timestep_embedding(const wam_timestep_args* args, void* stream);
+
+/* Linear over few rows on the vector ALUs (weight-streaming, any N and K):
+ *   out[r, n] = act_out(sum_k act_in(x[r, k]) * w[n, k] + bias[n])
+ * For the condition embedder, whose rows are one per (sample, frame)
+ * timestep: time_embedder.linear_1 + SiLU, linear_2 (fp32 weights, the
+ * model's _keep_in_fp32_modules), time_proj(SiLU(temb)); and action_proj_out
+ * (N = 30).  Rounding follows torch's per-op dtypes: act_in(x) is rounded to
+ * x's dtype; with act_out the pre-activation is rounded to the output dtype
+ * first.  Accumulation is fp32.  Rows are processed 8 at a time, so the
+ * weights are read ceil(R / 8) times: use wam_linear for many rows. */
+enum { WAM_ACT_NONE = 0, WAM_ACT_SILU = 1 };
+typedef struct {
+  const void* x; int x_dtype; int64_t ldx;  /* [R, K] WAM_F32 | WAM_BF16 */
+  const void* w; int w_dtype; int64_t ldw;  /* [N, K] WAM_F32 | WAM_BF16 */
+  const void* bias; int bias_dtype;         /* [N] or NULL */
+  void* out; int out_dtype; int64_t ldo;    /* [R, N] */
+  int R, N, K;
+  int act_in, act_out;                      /* WAM_ACT_* */
+} wam_rows_linear_args;
+
+int wam_rows_linear(const wam_rows_linear_args* args, void* stream);
+
+/* 3D RoPE frequencies (WanRotaryPosEmbed.forward, model.py:276-286):
+ * head_dim splits into f/h/w dims hd - 2*(hd/3), hd/3, hd/3 (44/42/42 for
+ * 128); pair j of axis a with dim d_a has base 1 / theta^(2j / d_a) (float64),
+ * angle = float(grid[b, a, l] * base) and out[b, l, pair] = (cos, sin) of it,
+ * complex64.  grid is [B, G >= 3, L] (rows frame, height, width, ...), dtype
+ * WAM_I64, WAM_F32 or WAM_F64. */
+typedef struct {
+  const void* grid; int grid_dtype;
+  int64_t grid_bstride, grid_rstride, grid_lstride; /* elements */
+  int B, L, head_dim;
+  double theta;
+  void* out;  /* complex64 [B, L, head_dim/2] */
+} wam_rope_freq_args;
+
+int wam_rope_freqs(const wam_rope_freq_args* args, void* stream);
 
 /* --------------------------------------------------------------- timing */
 /* Stage timer: pairs of HIP events recorded on the launch stream around

@@ -44,7 +44,9 @@ def test_linear_host_validation():
     assert "multiple of 64" in _err(h.wam_linear(ctypes.byref(a), None))
     a.K = a.lda = a.ldw = 128
     a.seg_n = 100
-    assert "multiple of 128" in _err(h.wam_linear(ctypes.byref(a), None))
+    assert "multiple of 8" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.seg_n, a.n_seg = 192, 2  # a partial last tile is fine for one segment only
+    assert "of 128 with several segments" in _err(h.wam_linear(ctypes.byref(a), None))
     a.seg_n, a.n_seg = 128, 4
     assert "n_seg" in _err(h.wam_linear(ctypes.byref(a), None))
     a.n_seg, a.epilogue = 1, _lib.EPI_BIAS_GATE_RES
@@ -93,3 +95,48 @@ def test_workspace_size():
     expect = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
               + R * 4)  # new-slot list
     assert expect <= n < expect + 4096
+
+
+def test_modulation_host_validation():
+    h = _lib.lib()
+    a = _lib.LnArgs()
+    a.x = a.y = 16
+    a.rows, a.D, a.eps = 12, 256, 1e-6
+    a.mod.table = a.mod.temb = 16
+    a.mod.tokens, a.mod.temb_len = 6, 4  # 4 does not divide 6
+    assert "divisor" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
+    a.mod.temb_len, a.mod.temb_mods = 3, 2
+    assert "mods" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
+    a.mod.temb_mods, a.shift_index = 1, 3  # a one-vector temb goes with the [2, D] head table
+    assert "shift index" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
+    a.mod.tokens = 5
+    assert "divisible by tokens" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
+
+
+def test_model_io_host_validation():
+    h = _lib.lib()
+    p = _lib.PatchifyArgs()
+    p.x = p.out = 16
+    p.B, p.C, p.F, p.H, p.W, p.p1, p.p2, p.p3, p.k_pad = 1, 48, 2, 9, 10, 1, 2, 2, 192
+    assert "multiples of the patch" in _err(h.wam_patchify(ctypes.byref(p), None))
+    p.H, p.k_pad = 8, 100
+    assert "k_pad" in _err(h.wam_patchify(ctypes.byref(p), None))
+    t = _lib.TimestepArgs()
+    t.t = t.out = 16
+    t.rows, t.dim, t.max_period, t.out_dtype = 4, 256, 10000.0, 7
+    assert "out dtype" in _err(h.wam_timestep_embedding(ctypes.byref(t), None))
+    r = _lib.RowsLinearArgs()
+    r.x = r.w = r.out = 16
+    r.R, r.N, r.K, r.ldx, r.ldw, r.ldo = 8, 30, 64, 64, 64, 30
+    r.w_dtype = _lib.WAM_FP8
+    assert "dtypes" in _err(h.wam_rows_linear(ctypes.byref(r), None))
+    r.w_dtype, r.ldw = _lib.WAM_BF16, 32
+    assert "strides" in _err(h.wam_rows_linear(ctypes.byref(r), None))
+    r.ldw, r.act_out = 64, 5
+    assert "activation" in _err(h.wam_rows_linear(ctypes.byref(r), None))
+    f = _lib.RopeFreqArgs()
+    f.grid = f.out = 16
+    f.grid_dtype, f.B, f.L, f.head_dim, f.theta = _lib.WAM_BF16, 1, 4, 128, 10000.0
+    assert "grid dtype" in _err(h.wam_rope_freqs(ctypes.byref(f), None))
+    f.grid_dtype, f.head_dim = _lib.WAM_I64, 130
+    assert "whole f/h/w pairs" in _err(h.wam_rope_freqs(ctypes.byref(f), None))

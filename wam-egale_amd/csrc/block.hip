@@ -160,8 +160,8 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   const int R = B * M;
   WAM_REQUIRE(B >= 1 && M >= 1, "block: empty input B=%d M=%d", B, M);
   WAM_REQUIRE(a->x && a->out, "block: null x/out");
-  WAM_REQUIRE(a->mod.temb && (a->mod.temb_len == 1 || a->mod.temb_len == M) && a->mod.tokens == M,
-              "block: temb must be [B, 1 or M, 6, D]");
+  WAM_TRY(check_modulation(a->mod, R, "block"));
+  WAM_REQUIRE(a->mod.tokens == M && a->mod.temb_mods != 1, "block: temb must be [B, L, 6, D] over M tokens");
   const bool precomputed = a->cross_k && a->cross_v;
   WAM_REQUIRE(a->context_batch >= 1 && a->context_len >= 1, "block: context shape");
   WAM_REQUIRE(precomputed || a->context, "block: context or precomputed cross K/V required");
@@ -403,6 +403,10 @@ size_t wam_abi_struct_size(const char* name) {
   if (!strcmp(name, "wam_kv_commit_args")) return sizeof(wam_kv_commit_args);
   if (!strcmp(name, "wam_block_weights")) return sizeof(wam_block_weights);
   if (!strcmp(name, "wam_block_args")) return sizeof(wam_block_args);
+  if (!strcmp(name, "wam_patchify_args")) return sizeof(wam_patchify_args);
+  if (!strcmp(name, "wam_timestep_args")) return sizeof(wam_timestep_args);
+  if (!strcmp(name, "wam_rows_linear_args")) return sizeof(wam_rows_linear_args);
+  if (!strcmp(name, "wam_rope_freq_args")) return sizeof(wam_rope_freq_args);
   return 0;
 }
 

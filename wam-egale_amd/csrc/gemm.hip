@@ -84,10 +84,7 @@ __device__ inline int lds_off(int r, int c) {
 
 __device__ inline void ld_mod4(const wam_modulation m, int D, int64_t row, int idx,
                                int d, float out[4]) {
-  int64_t b, t;
-  split_row(row, m.tokens, b, t);
-  const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
-  const int64_t toff = (trow * 6 + idx) * (int64_t)D + d;
+  const int64_t toff = temb_off(m, temb_row(m, row), idx, D, d);
   const int64_t tab = (int64_t)idx * D + d;
   if (m.table_dtype == WAM_F32) {
     float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(m.table) + tab);
@@ -546,10 +543,9 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   else
     WAM_REQUIRE(a->out_dtype == WAM_BF16, "wam_linear: fp32 output only for residual epilogues");
   if (a->epilogue == WAM_EPI_BIAS_GATE_RES) {
-    WAM_REQUIRE(a->gate.table && a->gate.temb && a->gate.tokens > 0 &&
-                (a->gate.temb_len == 1 || a->gate.temb_len == a->gate.tokens) &&
-                a->gate_index >= 0 && a->gate_index < 6 && a->M % a->gate.tokens == 0,
-                "wam_linear: gate modulation contract");
+    WAM_TRY(check_modulation(a->gate, a->M, "wam_linear"));
+    WAM_REQUIRE(a->gate.temb_mods != 1 && a->gate_index >= 0 && a->gate_index < 6,
+                "wam_linear: the gate reads a [.., 6, D] temb (index %d)", a->gate_index);
   }
   LinearParams p{};
   p.a = static_cast<const bf16*>(a->a); p.lda = a->lda; p.M = a->M; p.K = a->K;

@@ -63,13 +63,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args 
   const int64_t row = first + (threadIdx.x >> 6);
   const int D = a.D, nch = D >> 3;
   // Do all rows of this workgroup use the same coefficients?
-  bool shared = a.affine != 0;
-  if (!shared && a.mod.temb_len == 1) {
-    int64_t b0, b1, t0, t1;
-    split_row(first, a.mod.tokens, b0, t0);
-    split_row(last, a.mod.tokens, b1, t1);
-    shared = b0 == b1;
-  }
+  const bool shared = a.affine != 0 || temb_row(a.mod, first) == temb_row(a.mod, last);
   if (shared) {
     for (int ch = threadIdx.x; ch < nch; ch += 64 * kLnWaves) {
       float mul[8], add[8];
@@ -144,10 +138,10 @@ int ln_modulate(const wam_ln_args* a, hipStream_t s) {
   if (a->affine) {
     WAM_REQUIRE(a->gamma && a->beta, "wam_ln_modulate: affine needs gamma and beta");
   } else {
-    WAM_REQUIRE(a->mod.table && a->mod.temb && a->mod.tokens > 0 &&
-                (a->mod.temb_len == 1 || a->mod.temb_len == a->mod.tokens) &&
-                a->rows % a->mod.tokens == 0 && (a->shift_index == 0 || a->shift_index == 3),
-                "wam_ln_modulate: modulation contract (shift index %d)", a->shift_index);
+    WAM_TRY(check_modulation(a->mod, a->rows, "wam_ln_modulate"));
+    WAM_REQUIRE((a->shift_index == 0 || a->shift_index == 3) && (a->mod.temb_mods != 1 || a->shift_index == 0),
+                "wam_ln_modulate: shift index %d (0 with a one-vector temb and a [2, D] table)",
+                a->shift_index);
   }
   if (a->rows == 0) return WAM_OK;
   if (a->x_dtype == WAM_F32) launch_ln<true>(a, s);

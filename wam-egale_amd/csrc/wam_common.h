@@ -50,6 +50,21 @@ void set_error(const char* fmt, ...);
     if (rc_ != WAM_OK) return rc_; \
   } while (0)
 
+// Host-side contract of a modulation source read over `rows` token rows.
+inline int check_modulation(const wam_modulation& m, int64_t rows, const char* who) {
+  WAM_REQUIRE(m.table && m.temb && m.tokens > 0 && rows % m.tokens == 0,
+              "%s: modulation needs table, temb and rows (%lld) divisible by tokens (%d)", who,
+              (long long)rows, m.tokens);
+  WAM_REQUIRE(m.temb_len >= 1 && m.temb_len <= m.tokens && m.tokens % m.temb_len == 0,
+              "%s: temb length %d must be 1, the token count %d or a divisor of it", who, m.temb_len,
+              m.tokens);
+  WAM_REQUIRE(m.temb_mods == 0 || m.temb_mods == 6 || m.temb_mods == 1, "%s: temb mods %d must be 6 or 1",
+              who, m.temb_mods);
+  WAM_REQUIRE((m.table_dtype == WAM_F32 || m.table_dtype == WAM_BF16) &&
+              (m.temb_dtype == WAM_F32 || m.temb_dtype == WAM_BF16), "%s: modulation dtypes", who);
+  return WAM_OK;
+}
+
 // Workgroup i is dispatched to XCD i % 8 on MI355X.  Remap so that each XCD
 // receives one contiguous range of logical ids (bijective for any n).
 __host__ __device__ inline int xcd_remap(int i, int n) {
@@ -186,13 +201,24 @@ __device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[
     for (int e = 0; e < 8; ++e) out[e] = static_cast<float>(v[e]);
   }
 }
-__device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx, int d, float out[8]) {
+// Row of temb that serves token row `row`: per sample, per token, or per
+// group of tokens / temb_len consecutive tokens (one latent frame).
+__device__ inline int64_t temb_row(const wam_modulation& m, int64_t row) {
   int64_t b, t;
   split_row(row, m.tokens, b, t);
-  const int64_t trow = b * m.temb_len + (m.temb_len == 1 ? 0 : t);
+  if (m.temb_len == 1) return b;
+  if (m.temb_len == m.tokens) return b * m.tokens + t;
+  const uint32_t group = (uint32_t)m.tokens / (uint32_t)m.temb_len;
+  return b * m.temb_len + (uint32_t)t / group;
+}
+// Element offset of temb[trow, idx, d]: [.., 6, D] rows, or one vector per row.
+__device__ inline int64_t temb_off(const wam_modulation& m, int64_t trow, int idx, int D, int d) {
+  return m.temb_mods == 1 ? trow * D + d : (trow * 6 + idx) * (int64_t)D + d;
+}
+__device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx, int d, float out[8]) {
   float tb[8];
   ld8_f32(m.table, m.table_dtype, (int64_t)idx * D + d, out);
-  ld8_f32(m.temb, m.temb_dtype, (trow * 6 + idx) * (int64_t)D + d, tb);
+  ld8_f32(m.temb, m.temb_dtype, temb_off(m, temb_row(m, row), idx, D, d), tb);
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] += tb[e];
 }

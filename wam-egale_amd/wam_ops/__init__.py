@@ -11,6 +11,7 @@ from .whole_layer import WholeLayerBlock
 from .verify import BlockStack
 from .block import TransformerBlock
 from .parameters import Attention
+from .model import TransformerModel, WholeModel
 
 __all__ = ["install_block", "install_model", "NativeBlock", "WholeLayerBlock", "BlockStack",
-           "TransformerBlock", "Attention"]
+           "TransformerBlock", "Attention", "TransformerModel", "WholeModel"]

@@ -6,7 +6,7 @@ There is no fallback: if the library is missing, every entry point raises.
 """
 import ctypes
 import os
-from ctypes import (POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int64,
+from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64,
                     c_size_t, c_uint32, c_void_p)
 from functools import lru_cache
 from pathlib import Path
@@ -15,7 +15,8 @@ LIB_NAME = "libwam_block.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 WAM_OK, WAM_ERR_ARG, WAM_ERR_HIP, WAM_ERR_STATE = 0, -1, -2, -3
-WAM_BF16, WAM_F32, WAM_FP8 = 0, 1, 2
+WAM_BF16, WAM_F32, WAM_FP8, WAM_I64, WAM_F64 = 0, 1, 2, 3, 4
+WAM_ACT_NONE, WAM_ACT_SILU = 0, 1
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATE_RES, EPI_BIAS_RES = 0, 1, 2, 3
 DEBUG_SLOTS = 16
 STAGES = ("ln1", "qkv", "rms_rope", "kv_layout", "self_attn", "self_out", "ln2",
@@ -28,7 +29,8 @@ DEBUG_NAMES = ("modulated1", "self_q_rope", "self_k_rope", "self_v", "self_atten
 
 class Modulation(Structure):
     _fields_ = [("table", c_void_p), ("table_dtype", c_int), ("temb", c_void_p),
-                ("temb_dtype", c_int), ("temb_len", c_int), ("tokens", c_int)]
+                ("temb_dtype", c_int), ("temb_len", c_int), ("tokens", c_int),
+                ("temb_mods", c_int)]
 
 
 class LinearArgs(Structure):
@@ -97,11 +99,37 @@ class BlockArgs(Structure):
                 ("workspace_bytes", c_size_t), ("debug", c_void_p), ("timer", c_void_p)]
 
 
+class PatchifyArgs(Structure):
+    _fields_ = [("x", c_void_p), ("out", c_void_p), ("B", c_int), ("C", c_int), ("F", c_int),
+                ("H", c_int), ("W", c_int), ("p1", c_int), ("p2", c_int), ("p3", c_int),
+                ("k_pad", c_int)]
+
+
+class TimestepArgs(Structure):
+    _fields_ = [("t", c_void_p), ("rows", c_int), ("dim", c_int), ("flip_sin_to_cos", c_int),
+                ("shift", c_float), ("max_period", c_float), ("out", c_void_p), ("out_dtype", c_int)]
+
+
+class RowsLinearArgs(Structure):
+    _fields_ = [("x", c_void_p), ("x_dtype", c_int), ("ldx", c_int64), ("w", c_void_p),
+                ("w_dtype", c_int), ("ldw", c_int64), ("bias", c_void_p), ("bias_dtype", c_int),
+                ("out", c_void_p), ("out_dtype", c_int), ("ldo", c_int64), ("R", c_int), ("N", c_int),
+                ("K", c_int), ("act_in", c_int), ("act_out", c_int)]
+
+
+class RopeFreqArgs(Structure):
+    _fields_ = [("grid", c_void_p), ("grid_dtype", c_int), ("grid_bstride", c_int64),
+                ("grid_rstride", c_int64), ("grid_lstride", c_int64), ("B", c_int), ("L", c_int),
+                ("head_dim", c_int), ("theta", c_double), ("out", c_void_p)]
+
+
 STRUCTS = {
     "wam_modulation": Modulation, "wam_linear_args": LinearArgs, "wam_ln_args": LnArgs,
     "wam_rms_rope_args": RmsRopeArgs, "wam_attention_args": AttentionArgs,
     "wam_kv_layout_args": KvLayoutArgs, "wam_kv_commit_args": KvCommitArgs,
     "wam_block_weights": BlockWeights, "wam_block_args": BlockArgs,
+    "wam_patchify_args": PatchifyArgs, "wam_timestep_args": TimestepArgs,
+    "wam_rows_linear_args": RowsLinearArgs, "wam_rope_freq_args": RopeFreqArgs,
 }
 
 # Every symbol include/wam_block.h declares, with its ctypes signature.
@@ -118,6 +146,10 @@ SIGNATURES = {
     "wam_block_forward": (c_int, [POINTER(BlockArgs), c_void_p]),
     "wam_prepare_context": (c_int, [POINTER(BlockWeights), c_void_p, c_int, c_void_p, c_void_p,
                                     c_void_p]),
+    "wam_patchify": (c_int, [POINTER(PatchifyArgs), c_void_p]),
+    "wam_timestep_embedding": (c_int, [POINTER(TimestepArgs), c_void_p]),
+    "wam_rows_linear": (c_int, [POINTER(RowsLinearArgs), c_void_p]),
+    "wam_rope_freqs": (c_int, [POINTER(RopeFreqArgs), c_void_p]),
     "wam_timer_create": (c_void_p, [c_int, c_uint32]),
     "wam_timer_reset": (None, [c_void_p]),
     "wam_timer_read": (c_int, [c_void_p, POINTER(c_int32), POINTER(c_float), c_int]),

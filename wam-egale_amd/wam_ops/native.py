@@ -108,8 +108,8 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     _check(ctx.device == dev and ctx.dtype == torch.bfloat16 and ctx.is_contiguous()
            and ctx.dim() == 3 and ctx.shape[2] == D, "context must be [Bc, Lc, D] contiguous bf16")
     _check(temb.device == dev and temb.dim() == 4 and temb.shape[0] == B and temb.shape[2] == 6
-           and temb.shape[3] == D and temb.shape[1] in (1, M),
-           "temb must be [B, 1 or M, 6, D]")
+           and temb.shape[3] == D and temb.shape[1] >= 1 and M % temb.shape[1] == 0,
+           "temb must be [B, L, 6, D] with L = 1, M, or a divisor of M (one row per frame)")
     temb = temb.contiguous()
     table = bound.tensors[0]
     args = _lib.BlockArgs()
@@ -121,6 +121,7 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     mod = _lib.Modulation()
     mod.table, mod.table_dtype = table.data_ptr(), dtype_code(table)
     mod.temb, mod.temb_dtype, mod.temb_len, mod.tokens = temb.data_ptr(), dtype_code(temb), temb.shape[1], M
+    mod.temb_mods = 6
     args.mod = mod
     freq = None
     if rotary_emb is not None:

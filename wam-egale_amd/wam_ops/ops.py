@@ -15,7 +15,8 @@ from ._lib import (EPI_BIAS, EPI_BIAS_GATE_RES, EPI_BIAS_GELU, EPI_BIAS_RES, WAM
                    WAM_F32)
 
 __all__ = ["linear", "ln_modulate", "layer_norm_affine", "rms_rope", "attention",
-           "kv_layout", "kv_commit", "modulation", "stream_handle",
+           "kv_layout", "kv_commit", "modulation", "stream_handle", "patchify",
+           "timestep_embedding", "rows_linear", "rope_freqs", "head_norm",
            "EPI_BIAS", "EPI_BIAS_GELU", "EPI_BIAS_GATE_RES", "EPI_BIAS_RES"]
 
 
@@ -57,18 +58,28 @@ def _bf16(t, name):
 
 
 def modulation(table, temb, tokens):
-    """Describe mod = table[6, D] + temb[B, L, 6, D] for the C side.
+    """Describe mod = table + temb for the C side.
 
-    table may be [1, 6, D] or [6, D] (model.py:738-739); temb is
-    [B, 1 or tokens, 6, D] (model.py:751-759)."""
+    Block modulation: table [1, 6, D] or [6, D] (model.py:738-739), temb
+    [B, L, 6, D] (model.py:751-759).  Output head: table [1, 2, D], temb
+    [B, L, D], one vector for both shift and scale (model.py:1096-1101).
+    L is 1 (per sample), the token count (per token), or a divisor of it: each
+    temb row then serves tokens / L consecutive tokens (one latent frame)."""
     _req(table.is_contiguous() and temb.is_contiguous(), "table/temb must be contiguous")
-    _req(temb.dim() == 4 and temb.shape[2] == 6, "temb must be [B, L, 6, D]")
-    _req(temb.shape[1] in (1, tokens), "temb length must be 1 or the token count")
-    _req(table.numel() == 6 * temb.shape[3], "scale_shift_table must hold 6 x D values")
+    if temb.dim() == 3:
+        mods, D = 1, temb.shape[2]
+        _req(table.numel() == 2 * D, "the output head's scale_shift_table must hold 2 x D values")
+    else:
+        _req(temb.dim() == 4 and temb.shape[2] == 6, "temb must be [B, L, 6, D]")
+        mods, D = 6, temb.shape[3]
+        _req(table.numel() == 6 * D, "scale_shift_table must hold 6 x D values")
+    L = temb.shape[1]
+    _req(L >= 1 and tokens % L == 0,
+         "temb length must be 1, the token count, or a divisor of it (one row per frame)")
     m = _lib.Modulation()
     m.table, m.table_dtype = table.data_ptr(), dtype_code(table)
     m.temb, m.temb_dtype = temb.data_ptr(), dtype_code(temb)
-    m.temb_len, m.tokens = temb.shape[1], tokens
+    m.temb_len, m.tokens, m.temb_mods = L, tokens, mods
     return m
 
 
@@ -304,3 +315,112 @@ def kv_commit(cache, k, v, new_slots):
     a.pool_bstride, a.pool_rstride = cache["k"].stride(0), cache["k"].stride(1)
     a.new_slots, a.B, a.tokens, a.D = new_slots.data_ptr(), B, M, D
     _lib.check(_lib.lib().wam_kv_commit(ctypes.byref(a), stream_handle(dev)), "wam_kv_commit")
+
+
+# ---------------------------------------------------------- model input / output
+def patchify(latents, patch, k_pad=None, out=None):
+    """'b c (f p1) (h p2) (w p3) -> b (f h w) (c p1 p2 p3)' of bf16 latents
+    [B, C, F, H, W] (model.py:1064-1069; patch (1, 1, 1) is the action path's
+    'b c f h w -> b (f h w) c').  Returns [B, L, k_pad] bf16 whose columns
+    past C*p1*p2*p3 are zero (k_pad defaults to that product)."""
+    dev = _dev(latents)
+    _bf16(latents, "latents")
+    _req(latents.dim() == 5 and latents.is_contiguous(), "latents must be [B, C, F, H, W] contiguous")
+    B, C, F, H, W = latents.shape
+    p1, p2, p3 = (int(v) for v in patch)
+    _req(F % p1 == 0 and H % p2 == 0 and W % p3 == 0, "latent F/H/W must be multiples of the patch")
+    K = C * p1 * p2 * p3
+    k_pad = K if k_pad is None else int(k_pad)
+    L = (F // p1) * (H // p2) * (W // p3)
+    y = out if out is not None else torch.empty(B, L, k_pad, dtype=torch.bfloat16, device=dev)
+    _req(y.dtype == torch.bfloat16 and y.is_contiguous() and y.numel() == B * L * k_pad, "out [B, L, k_pad]")
+    a = _lib.PatchifyArgs()
+    a.x, a.out = latents.data_ptr(), y.data_ptr()
+    a.B, a.C, a.F, a.H, a.W = B, C, F, H, W
+    a.p1, a.p2, a.p3, a.k_pad = p1, p2, p3, k_pad
+    _lib.check(_lib.lib().wam_patchify(ctypes.byref(a), stream_handle(dev)), "wam_patchify")
+    return y
+
+
+def timestep_embedding(t, dim=256, flip_sin_to_cos=True, shift=0.0, max_period=10000.0,
+                       out_dtype=torch.float32, out=None):
+    """diffusers Timesteps (get_timestep_embedding): t [R] fp32 -> [R, dim]."""
+    dev = _dev(t)
+    _req(t.dtype == torch.float32 and t.is_contiguous(), "timesteps must be contiguous float32")
+    R = t.numel()
+    y = out if out is not None else torch.empty(R, dim, dtype=out_dtype, device=dev)
+    _req(y.is_contiguous() and y.shape == (R, dim), "out must be [R, dim]")
+    a = _lib.TimestepArgs()
+    a.t, a.rows, a.dim, a.flip_sin_to_cos = t.data_ptr(), R, dim, int(bool(flip_sin_to_cos))
+    a.shift, a.max_period, a.out, a.out_dtype = shift, max_period, y.data_ptr(), dtype_code(y)
+    _lib.check(_lib.lib().wam_timestep_embedding(ctypes.byref(a), stream_handle(dev)),
+               "wam_timestep_embedding")
+    return y
+
+
+_ACTS = {None: _lib.WAM_ACT_NONE, "silu": _lib.WAM_ACT_SILU}
+
+
+def rows_linear(x, w, b=None, act_in=None, act_out=None, out_dtype=None, out=None):
+    """out = act_out(act_in(x) W^T + b) for few rows on the vector ALUs; x, w,
+    b and out may each be float32 or bfloat16 (torch's per-op roundings)."""
+    dev = _dev(x, w, b)
+    _req(x.dim() >= 1 and x.stride(-1) == 1 and w.dim() == 2 and w.stride(-1) == 1,
+         "x and w need contiguous rows")
+    K = x.shape[-1]
+    N = w.shape[0]
+    _req(w.shape[1] == K, f"weight must be [N, {K}]")
+    x2 = x.reshape(-1, K)
+    R = x2.shape[0]
+    _req(act_in in _ACTS and act_out in _ACTS, "activations: None or 'silu'")
+    y = out if out is not None else torch.empty(*x.shape[:-1], N, dtype=out_dtype or x.dtype, device=dev)
+    _req(y.is_contiguous() and y.numel() == R * N, "out must be [..., N] contiguous")
+    a = _lib.RowsLinearArgs()
+    a.x, a.x_dtype, a.ldx = x2.data_ptr(), dtype_code(x2), x2.stride(0)
+    a.w, a.w_dtype, a.ldw = w.data_ptr(), dtype_code(w), w.stride(0)
+    if b is not None:
+        _req(b.is_contiguous() and b.numel() == N, "bias must be [N]")
+        a.bias, a.bias_dtype = b.data_ptr(), dtype_code(b)
+    a.out, a.out_dtype, a.ldo = y.data_ptr(), dtype_code(y), N
+    a.R, a.N, a.K = R, N, K
+    a.act_in, a.act_out = _ACTS[act_in], _ACTS[act_out]
+    _lib.check(_lib.lib().wam_rows_linear(ctypes.byref(a), stream_handle(dev)), "wam_rows_linear")
+    return y
+
+
+def rope_freqs(grid_ids, head_dim=128, theta=10000.0, out=None):
+    """WanRotaryPosEmbed.forward: grid ids [B, >=3, L] (int64, float32 or
+    float64) -> complex64 [B, L, 1, head_dim/2] (model.py:276-286, with the
+    [:, :, None] of model.py:1077)."""
+    dev = _dev(grid_ids)
+    codes = {torch.int64: _lib.WAM_I64, torch.float32: _lib.WAM_F32, torch.float64: _lib.WAM_F64}
+    _req(grid_ids.dtype in codes, "grid ids must be int64, float32 or float64")
+    _req(grid_ids.dim() == 3 and grid_ids.shape[1] >= 3, "grid ids must be [B, >=3, L]")
+    B, _, L = grid_ids.shape
+    y = out if out is not None else torch.empty(B, L, 1, head_dim // 2, dtype=torch.complex64, device=dev)
+    _req(y.dtype == torch.complex64 and y.is_contiguous() and y.numel() == B * L * (head_dim // 2),
+         "out must be complex64 [B, L, 1, head_dim/2]")
+    a = _lib.RopeFreqArgs()
+    a.grid, a.grid_dtype = grid_ids.data_ptr(), codes[grid_ids.dtype]
+    a.grid_bstride, a.grid_rstride, a.grid_lstride = grid_ids.stride()
+    a.B, a.L, a.head_dim, a.theta, a.out = B, L, head_dim, theta, y.data_ptr()
+    _lib.check(_lib.lib().wam_rope_freqs(ctypes.byref(a), stream_handle(dev)), "wam_rope_freqs")
+    return y
+
+
+def head_norm(x, table, temb, eps=1e-6, out=None):
+    """norm_out + modulation of the output head (model.py:1096-1103):
+    bf16(LN(x) * (1 + table[1] + temb) + table[0] + temb), x [B, M, D],
+    table [1, 2, D] fp32, temb [B, L, D] with L dividing M."""
+    dev = _dev(x, table, temb)
+    _req(x.dim() == 3 and x.is_contiguous(), "x must be [B, M, D] contiguous")
+    B, M, D = x.shape
+    _req(temb.dim() == 3 and temb.shape[0] == B and temb.shape[2] == D, "temb must be [B, L, D]")
+    y = out if out is not None else torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    a = _lib.LnArgs()
+    a.x, a.y, a.rows, a.D, a.eps, a.affine = x.data_ptr(), y.data_ptr(), B * M, D, eps, 0
+    a.x_dtype = dtype_code(x)
+    a.mod = modulation(table, temb, M)
+    a.shift_index = 0
+    _lib.check(_lib.lib().wam_ln_modulate(ctypes.byref(a), stream_handle(dev)), "wam_ln_modulate")
+    return y
