@@ -183,11 +183,18 @@ def c4a_attention(shape, dev, steps, warmup, q_tokens=1560, prefix=6240):
 
 
 def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup, layers=30):
-    """C5: the 30-layer speculative verify forward (BlockStack) measured as a
-    whole: 30 random-init layers, each with its own 6240-token committed prefix
-    in pool row 0 and its own precomputed cross K/V; 4 candidates x 1560 tokens."""
+    """C5: the 30-layer speculative verify forward, measured two ways over the
+    same 30 random-init layers (each with its own 6240-token committed prefix
+    in pool row 0); 4 candidates x 1560 tokens:
+
+    stack30 - the block loop alone (BlockStack, precomputed cross K/V);
+    model30 - the whole WanTransformer3DModel forward (WholeModel): patch
+              embedding of [4, 48, 2, 52, 60] latents, RoPE from grid ids, the
+              condition embedder on the [4, 2] per-frame timesteps, the 30
+              blocks, norm_out + modulation and proj_out, with the 512 x 4096
+              text prepared once (text embedder + every layer's cross K/V)."""
     import torch
-    from wam_ops import BlockStack, synthetic
+    from wam_ops import BlockStack, TransformerModel, synthetic
     B, Mv = x.shape[0], x.shape[1]
     blocks = []
     for i in range(layers):
@@ -207,9 +214,44 @@ def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup,
     res = {"layers": layers, "ms_per_forward": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
            "tokens_per_s": round(B * Mv / (ms * 1e-3), 1),
            "tflops": round(layers * (g + a) / (ms * 1e-3) / 1e12, 1), "steps": steps, "warmup": warmup}
-    del stack, blocks
+    del stack
+
+    # the whole model over the same layers
+    with torch.device("meta"):
+        model = TransformerModel(num_attention_heads=shape.heads, attention_head_dim=shape.head_dim,
+                                 ffn_dim=shape.ffn, num_layers=0)
+    model.load_state_dict(synthetic.model_io_params(model, seed=7, device=dev), assign=True)
+    model.blocks = torch.nn.ModuleList(blocks)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    frames, hp, wp = 2, 26, 30
+    lat = torch.randn(B, 48, frames, 2 * hp, 2 * wp, generator=gen, device=dev).to(torch.bfloat16)
+    text = torch.randn(1, ctx.shape[1], 4096, generator=gen, device=dev).to(torch.bfloat16)
+    grid = synthetic.mesh_grid_ids(frames, hp, wp).to(torch.int64)
+    grid = torch.cat([grid, torch.zeros_like(grid[:1])])[None].repeat(B, 1, 1).to(dev)
+    inp = {"noisy_latents": lat, "text_emb": text.expand(B, -1, -1).clone(), "grid_id": grid,
+           "timesteps": torch.tensor([[0.0, 500.0 + 50 * k] for k in range(B)], device=dev)}
+    whole = model.native()
+    with torch.no_grad():
+        prep_ms = timed_steps(lambda: whole.prepare_text(inp["text_emb"]), 1, 1)
+
+        def model_step():
+            return whole(inp, candidate_cache_rows=rows)
+
+        def io_step():
+            xe = whole.embed(lat, False)
+            fr = whole._bind()
+            from wam_ops import ops
+            ops.rope_freqs(grid)
+            te, _ = fr["cond"].time(inp["timesteps"], xe.dtype)
+            return whole.head(xe, te, False)
+        mms = timed_steps(model_step, steps, warmup)
+        ims = timed_steps(io_step, steps, warmup)
+    res_model = {"ms_per_forward": round(mms, 3), "tokens_per_s": round(B * Mv / (mms * 1e-3), 1),
+                 "io_us": round(ims * 1e3, 1), "prepare_text_ms": round(prep_ms, 3),
+                 "latents": list(lat.shape), "text": [B, ctx.shape[1], 4096], "timesteps": [B, frames]}
+    del whole, model, blocks
     torch.cuda.empty_cache()
-    return res
+    return res, res_model
 
 
 def main():
@@ -341,8 +383,8 @@ def main():
                           "frac_of_bf16_peak": round((g + a) / (vms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                           "us_30_layers_extrapolated": round(30 * vms * 1e3, 1)}
         del vlayer
-        out["lverify"]["stack30"] = verify_stack30(shape, dev, xv, ctxv, tembv, freqv, rows, prefix,
-                                                   min(args.steps, 5), 2)
+        out["lverify"]["stack30"], out["lverify"]["model30"] = verify_stack30(
+            shape, dev, xv, ctxv, tembv, freqv, rows, prefix, min(args.steps, 5), 2)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(shape)
     print(json.dumps(out), flush=True)

@@ -334,9 +334,10 @@ int wam_timestep_embedding(const wam_timestep_args* args, void* stream);
  * timestep: time_embedder.linear_1 + SiLU, linear_2 (fp32 weights, the
  * model's _keep_in_fp32_modules), time_proj(SiLU(temb)); and action_proj_out
  * (N = 30).  Rounding follows torch's per-op dtypes: act_in(x) is rounded to
- * x's dtype; with act_out the pre-activation is rounded to the output dtype
- * first.  Accumulation is fp32.  Rows are processed 8 at a time, so the
- * weights are read ceil(R / 8) times: use wam_linear for many rows. */
+ * x's dtype (the input SiLU uses a hardware exp2/reciprocal, a few fp32 ulp);
+ * with act_out the pre-activation is rounded to the output dtype first.
+ * Accumulation is fp32.  Rows are processed 8 at a time, so the weights are
+ * read ceil(R / 8) times: use wam_linear for many rows. */
 enum { WAM_ACT_NONE = 0, WAM_ACT_SILU = 1 };
 typedef struct {
   const void* x; int x_dtype; int64_t ldx;  /* [R, K] WAM_F32 | WAM_BF16 */

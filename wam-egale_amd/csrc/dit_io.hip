@@ -109,15 +109,24 @@ int timestep_embedding(const wam_timestep_args* a, hipStream_t s) {
 }
 
 // ------------------------------------------------------------ rows_linear
-// Workgroup (256 threads) = a tile of kRlRows rows x kRlCols outputs.  Thread
-// t owns the k-chunks 8t, 8t + 2048, ...: it streams those 8-element pieces of
-// the tile's weight rows (coalesced 16-byte loads across the wave) and of the
-// tile's x rows (L2-resident: x is small), and keeps the 8x8 partial dot
-// products in registers.  Partials are summed within each wave (DPP) and then
-// across the 4 waves through LDS.
-constexpr int kRlRows = 8, kRlCols = 8, kRlThreads = 256;
+// Weight streaming: each wave owns kRlOut consecutive outputs (weight rows)
+// and up to kRlRows rows of x.  Lane l reads the 8-element pieces
+// k = 8l + 512j of its weight rows (16-byte loads, 1 KB per wave instruction,
+// straight from HBM) and of the x rows, and keeps the kRlRows x kRlOut
+// partial dot products in registers; one DPP reduction per output at the end.
+//
+// Without an input activation the x rows are read from L2 by every wave and
+// a workgroup is 4 independent waves.  With one (SiLU), act_in(x) is formed
+// once per workgroup of 8 waves into LDS, kRlSeg columns at a time, so the
+// activation is not recomputed per wave.
+constexpr int kRlRows = 8, kRlOut = 4, kRlSeg = 2048;
 
 __device__ inline float silu(float v) { return v / (1.f + expf(-v)); }
+// SiLU of an input element: v * rcp(1 + 2^(-v log2 e)); a few ulp of fp32,
+// below the bf16 rounding that follows for bf16 inputs.
+__device__ inline float silu_fast(float v) {
+  return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-v * kLog2e));
+}
 __device__ inline float round_to(float v, int dtype) {
   return dtype == WAM_BF16 ? static_cast<float>(static_cast<bf16>(v)) : v;
 }
@@ -133,63 +142,119 @@ __device__ inline void rl_load8(const void* p, int dtype, int64_t off, int left,
 }
 
 template <bool VEC>
-__global__ __launch_bounds__(kRlThreads) void rows_linear_kernel(wam_rows_linear_args a) {
-  __shared__ float red[kRlThreads / 64][kRlRows * kRlCols];
-  const int n0 = blockIdx.x * kRlCols, r0 = blockIdx.y * kRlRows;
-  const int nr = min(kRlRows, a.R - r0), nc = min(kRlCols, a.N - n0);
-  float acc[kRlRows][kRlCols];
+__device__ inline void rl_weights(const wam_rows_linear_args& a, int n0, int nc, int k, float wv[kRlOut][8]) {
 #pragma unroll
-  for (int r = 0; r < kRlRows; ++r)
+  for (int c = 0; c < kRlOut; ++c) {
+    if (c < nc) {
+      rl_load8<VEC>(a.w, a.w_dtype, (int64_t)(n0 + c) * a.ldw + k, a.K - k, wv[c]);
+    } else {
 #pragma unroll
-    for (int c = 0; c < kRlCols; ++c) acc[r][c] = 0.f;
-  for (int k = threadIdx.x * 8; k < a.K; k += kRlThreads * 8) {
-    const int left = a.K - k;
-    float xv[kRlRows][8];
-#pragma unroll
-    for (int r = 0; r < kRlRows; ++r) {
-      if (r < nr) {
-        rl_load8<VEC>(a.x, a.x_dtype, (int64_t)(r0 + r) * a.ldx + k, left, xv[r]);
-        if (a.act_in == WAM_ACT_SILU) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) xv[r][e] = round_to(silu(xv[r][e]), a.x_dtype);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[r][e] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < kRlCols; ++c) {
-      if (c >= nc) continue;
-      float wv[8];
-      rl_load8<VEC>(a.w, a.w_dtype, (int64_t)(n0 + c) * a.ldw + k, left, wv);
-#pragma unroll
-      for (int r = 0; r < kRlRows; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][c] += xv[r][e] * wv[e];
+      for (int e = 0; e < 8; ++e) wv[c][e] = 0.f;
     }
   }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+}
+
+__device__ inline void rl_fma(float acc[kRlRows][kRlOut], int r, const float xv[8], const float wv[kRlOut][8]) {
+#pragma unroll
+  for (int c = 0; c < kRlOut; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][c] += xv[e] * wv[c][e];
+}
+
+__device__ inline void rl_store(const wam_rows_linear_args& a, float acc[kRlRows][kRlOut], int lane, int n0,
+                                int r0, int nr, int nc) {
+  // Lane r * kRlOut + c keeps the sum of output (r, c).
+  float mine = 0.f;
 #pragma unroll
   for (int r = 0; r < kRlRows; ++r)
 #pragma unroll
-    for (int c = 0; c < kRlCols; ++c) {
+    for (int c = 0; c < kRlOut; ++c) {
       const float v = wave_sum(acc[r][c]);
-      if (lane == 0) red[wave][r * kRlCols + c] = v;
+      if (lane == r * kRlOut + c) mine = v;
     }
-  __syncthreads();
-  if (threadIdx.x >= kRlRows * kRlCols) return;
-  const int r = threadIdx.x / kRlCols, c = threadIdx.x % kRlCols;
-  if (r >= nr || c >= nc) return;
-  float v = 0.f;
-#pragma unroll
-  for (int w = 0; w < kRlThreads / 64; ++w) v += red[w][threadIdx.x];
+  const int r = lane / kRlOut, c = lane % kRlOut;
+  if (lane >= kRlRows * kRlOut || r >= nr || c >= nc) return;
   const int n = n0 + c;
+  float v = mine;
   if (a.bias) v += ld_scalar(a.bias, a.bias_dtype, n);
   if (a.act_out == WAM_ACT_SILU) v = silu(round_to(v, a.out_dtype));
   const int64_t o = (int64_t)(r0 + r) * a.ldo + n;
   if (a.out_dtype == WAM_F32) static_cast<float*>(a.out)[o] = v;
   else static_cast<bf16*>(a.out)[o] = static_cast<bf16>(v);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void rows_linear_kernel(wam_rows_linear_args a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * kRlOut;
+  const int r0 = blockIdx.y * kRlRows;
+  if (n0 >= a.N) return;  // whole wave; nothing below synchronises
+  const int nr = min(kRlRows, a.R - r0), nc = min(kRlOut, a.N - n0);
+  float acc[kRlRows][kRlOut];
+#pragma unroll
+  for (int r = 0; r < kRlRows; ++r)
+#pragma unroll
+    for (int c = 0; c < kRlOut; ++c) acc[r][c] = 0.f;
+  for (int k = lane * 8; k < a.K; k += 512) {
+    float wv[kRlOut][8];
+    rl_weights<VEC>(a, n0, nc, k, wv);
+#pragma unroll
+    for (int r = 0; r < kRlRows; ++r) {
+      if (r >= nr) continue;
+      float xv[8];
+      rl_load8<VEC>(a.x, a.x_dtype, (int64_t)(r0 + r) * a.ldx + k, a.K - k, xv);
+      rl_fma(acc, r, xv, wv);
+    }
+  }
+  rl_store(a, acc, lane, n0, r0, nr, nc);
+}
+
+// With act_in: 8 waves share act_in(x) staged in LDS (fp32, rounded to x's dtype).
+template <bool VEC>
+__global__ __launch_bounds__(512) void rows_linear_act_kernel(wam_rows_linear_args a) {
+  __shared__ __attribute__((aligned(16))) float xs[kRlRows][kRlSeg];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 8 + wave) * kRlOut;
+  const int r0 = blockIdx.y * kRlRows;
+  const int nr = min(kRlRows, a.R - r0), nc = max(0, min(kRlOut, a.N - n0));
+  float acc[kRlRows][kRlOut];
+#pragma unroll
+  for (int r = 0; r < kRlRows; ++r)
+#pragma unroll
+    for (int c = 0; c < kRlOut; ++c) acc[r][c] = 0.f;
+  for (int seg = 0; seg < a.K; seg += kRlSeg) {
+    const int len = min(kRlSeg, a.K - seg);
+    __syncthreads();  // the previous segment is no longer read
+    for (int i = threadIdx.x * 8; i < kRlRows * kRlSeg; i += 512 * 8) {
+      const int r = i / kRlSeg, k = i % kRlSeg;
+      float v[8];
+      if (r < nr && k < len) {
+        rl_load8<VEC>(a.x, a.x_dtype, (int64_t)(r0 + r) * a.ldx + seg + k, len - k, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = round_to(silu_fast(v[e]), a.x_dtype);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+      *reinterpret_cast<float4*>(&xs[r][k]) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(&xs[r][k + 4]) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+    if (nc == 0) continue;  // wave past N: keeps joining the barriers
+    for (int k = lane * 8; k < len; k += 512) {
+      float wv[kRlOut][8];
+      rl_weights<VEC>(a, n0, nc, seg + k, wv);
+#pragma unroll
+      for (int r = 0; r < kRlRows; ++r) {
+        if (r >= nr) continue;
+        const float4 p = *reinterpret_cast<const float4*>(&xs[r][k]);
+        const float4 q = *reinterpret_cast<const float4*>(&xs[r][k + 4]);
+        const float xv[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+        rl_fma(acc, r, xv, wv);
+      }
+    }
+  }
+  if (nc > 0) rl_store(a, acc, lane, n0, r0, nr, nc);
 }
 
 static bool fd(int d) { return d == WAM_F32 || d == WAM_BF16; }
@@ -208,9 +273,16 @@ int rows_linear(const wam_rows_linear_args* a, hipStream_t s) {
   // 16-byte vector loads need 8-element chunks that start 16-byte aligned.
   const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   const bool vec = a->K % 8 == 0 && a->ldx % 8 == 0 && a->ldw % 8 == 0 && al(a->x) && al(a->w);
-  const dim3 grid((unsigned)((a->N + kRlCols - 1) / kRlCols), (unsigned)((a->R + kRlRows - 1) / kRlRows));
-  if (vec) hipLaunchKernelGGL(rows_linear_kernel<true>, grid, dim3(kRlThreads), 0, s, *a);
-  else hipLaunchKernelGGL(rows_linear_kernel<false>, grid, dim3(kRlThreads), 0, s, *a);
+  const bool act = a->act_in != WAM_ACT_NONE;
+  const int per_wg = kRlOut * (act ? 8 : 4);
+  const dim3 grid((unsigned)((a->N + per_wg - 1) / per_wg), (unsigned)((a->R + kRlRows - 1) / kRlRows));
+  if (act) {
+    if (vec) hipLaunchKernelGGL(rows_linear_act_kernel<true>, grid, dim3(512), 0, s, *a);
+    else hipLaunchKernelGGL(rows_linear_act_kernel<false>, grid, dim3(512), 0, s, *a);
+  } else {
+    if (vec) hipLaunchKernelGGL(rows_linear_kernel<true>, grid, dim3(256), 0, s, *a);
+    else hipLaunchKernelGGL(rows_linear_kernel<false>, grid, dim3(256), 0, s, *a);
+  }
   WAM_LAUNCHED("rows_linear_kernel");
   return WAM_OK;
 }

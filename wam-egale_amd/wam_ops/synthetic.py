@@ -80,6 +80,25 @@ def block_params(shape: BlockShape, seed=0, device="cpu", dtype=torch.bfloat16, 
     return p
 
 
+def model_io_params(model, seed=0, device="cpu", dtype=torch.bfloat16):
+    """state_dict-named values for every model parameter outside the blocks:
+    N(0, 0.02) weights and biases, fp32 for time_embedder (the model's
+    _keep_in_fp32_modules, model.py:809-821) and `dtype` otherwise;
+    scale_shift_table N(0, 1)/sqrt(D) in fp32 (model.py:878-879)."""
+    p = {}
+    for i, (name, prm) in enumerate(sorted(model.named_parameters())):
+        if name.startswith("blocks."):
+            continue
+        if name == "scale_shift_table":
+            p[name] = _normal(tuple(prm.shape), 0.0, 1.0 / math.sqrt(prm.shape[-1]), device, seed, 500 + i,
+                              torch.float32)
+        elif "time_embedder" in name:
+            p[name] = _normal(tuple(prm.shape), 0.0, 0.02, device, seed, 500 + i, torch.float32)
+        else:
+            p[name] = _normal(tuple(prm.shape), 0.0, 0.02, device, seed, 500 + i, dtype)
+    return p
+
+
 def mesh_grid_ids(f, h, w):
     """[3, f*h*w] (frame, row, col) ids in raster order (utils.get_mesh_id)."""
     ff, hh, ww = torch.meshgrid(torch.arange(f), torch.arange(h), torch.arange(w), indexing="ij")
