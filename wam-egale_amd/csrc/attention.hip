@@ -121,7 +121,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
       const int c = is_k ? (pch ^ (row & 15)) : (pch ^ ((row & 3) << 2));
       const bf16* src = j < n_hist ? (is_k ? pool_k : pool_v) + (int64_t)slot * a.pool_rstride
                                    : (is_k ? own_k : own_v) + (int64_t)(j - n_hist) * a.kv_rstride;
-      g_ld16_lds(src + c * 8, base + (is_k ? 0 : kAttnTile) + gb * 1024);
+      asm_g_ld16_lds((uint64_t)(uintptr_t)(src + c * 8), base + (is_k ? 0 : kAttnTile) + gb * 1024);
     }
   };
 
@@ -166,16 +166,30 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
       const char* vb = kb + kAttnTile;
 
       // The two 32-key halves alternate, so consecutive MFMAs never wait on
-      // each other's accumulator.
+      // each other's accumulator.  K fragments are read two k-steps ahead of
+      // their MFMAs, so an LDS read has two steps of MFMAs to land.
       f32x16 s[2];
       s[0] = f32x16{};
       s[1] = f32x16{};
+      bf16x8 kf[3][2];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) kf[ks][kt] = ld_bf16x8(kb + k_off(kt * 32 + l32, 2 * ks + half));
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first two steps' reads
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        if (ks + 2 < 8) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+            kf[(ks + 2) % 3][kt] = ld_bf16x8(kb + k_off(kt * 32 + l32, 2 * (ks + 2) + half));
+        }
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
-          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ld_bf16x8(kb + k_off(kt * 32 + l32, 2 * ks + half)),
-                                                          qf[ks], s[kt], 0, 0, 0);
+          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3][kt], qf[ks], s[kt], 0, 0, 0);
+        if (ks + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // the reads two steps ahead
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                  // then this step's MFMAs
+      }
       if ((t_first + t + 1) * kAttnKT > n_tot) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -185,57 +199,68 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
             if (j >= n_tot) s[kt][v] = -INFINITY;
           }
       }
+      // Lazy rescaling: the running max m_run (log2 units, equal in both
+      // lane halves of a query) only moves when a tile's max exceeds it by
+      // more than 8, so exp2(s - m_run) <= 2^8.  A lane's own 32 keys decide
+      // whether anything moved; only then are the halves' maxima exchanged,
+      // the new running max set and O/l rescaled (the first tile, and rare
+      // jumps after it).  sum(p v) / sum(p) does not depend on which max is
+      // used.
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kt][v]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // Lazy rescaling: the running max m_run only moves when this tile's max
-      // exceeds it by more than 2^8 (log2 units), so exp2(s - m_run) <= 2^8;
-      // the O/l rescale runs only when some lane's max moved.  The result
-      // sum(p v) / sum(p) does not depend on which max is used.
-      const float mt = mx * sc;
-      const bool grow = mt > m_run + 8.0f;
-      const float m_new = grow ? mt : m_run;
+      if (__builtin_amdgcn_ballot_w64(mx * sc > m_run + 8.0f)) {
+        const float mt = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sc;
+        const bool grow = mt > m_run + 8.0f;
+        const float m_new = grow ? mt : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        m_run = m_new;
+      }
       float psum = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float pv = __builtin_amdgcn_exp2f(s[kt][v] * sc - m_new);
+          const float pv = __builtin_amdgcn_exp2f(s[kt][v] * sc - m_run);
           s[kt][v] = pv;
           psum += pv;
         }
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-      }
       l_run += psum;
-      m_run = m_new;
 
       bf16x8 pb[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int u = 0; u < 8; ++u) pb[ks][u] = static_cast<bf16>(s[ks >> 1][(ks & 1) * 8 + u]);
+      // V^T fragments (two transposed reads each) are read two MFMAs ahead.
+      auto vload = [&](int i) {
+        const int ks = i >> 2, dt = i & 3;
+        bf16x8 va;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          bf16x8 va;
-#pragma unroll
-          for (int part = 0; part < 2; ++part) {
-            const int key = 16 * ks + 4 * half + 8 * part + (tr_i >> 2);
-            const int d = 32 * dt + 16 * tr_gh + 4 * (tr_i & 3);
-            const bf16x4 t4 = ld_tr16(vb + v_off(key, d >> 3) + (d & 7) * 2);
-            va[4 * part + 0] = t4[0]; va[4 * part + 1] = t4[1];
-            va[4 * part + 2] = t4[2]; va[4 * part + 3] = t4[3];
-          }
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[ks], o[dt], 0, 0, 0);
+        for (int part = 0; part < 2; ++part) {
+          const int key = 16 * ks + 4 * half + 8 * part + (tr_i >> 2);
+          const int d = 32 * dt + 16 * tr_gh + 4 * (tr_i & 3);
+          const bf16x4 t4 = ld_tr16(vb + v_off(key, d >> 3) + (d & 7) * 2);
+          va[4 * part + 0] = t4[0]; va[4 * part + 1] = t4[1];
+          va[4 * part + 2] = t4[2]; va[4 * part + 3] = t4[3];
         }
+        return va;
+      };
+      bf16x8 vf[3];
+      vf[0] = vload(0);
+      vf[1] = vload(1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i + 2 < 16) vf[(i + 2) % 3] = vload(i + 2);
+        o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[i % 3], pb[i >> 2], o[i & 3], 0, 0, 0);
+        if (i + 2 < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
     }
   }
