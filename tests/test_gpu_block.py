@@ -59,6 +59,50 @@ def test_block_vs_fp32_oracle(dev, cfg, B, grid, Lc, per_token):
     print("block parity", cfg, grid, m)
 
 
+def test_block_l4680_headline(dev):
+    """The measured workload itself: one Wan2.2-5B block, B=1, 4680 tokens
+    (RoPE grid 6x26x30), 512 text tokens with precomputed cross K/V, against
+    the fp32 oracle at the block bound."""
+    from wam_ops import synthetic
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = synthetic.WAN22_5B
+    params = synthetic.block_params(shape, seed=1)
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4680, (6, 26, 30), context_len=512, seed=1)
+    wl = WholeLayerBlock(native_block(params, shape, dev))
+    with torch.no_grad():
+        wl.prepare_context(ctx.to(dev), precompute=True)
+        out = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+    torch.cuda.synchronize()
+    ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
+    m = assert_close(out.cpu(), ref, max_abs=2e-2, min_cos=0.9999, what="L4680 block")
+    print("L4680 parity", m)
+
+
+def test_verify_layer_full_size(dev):
+    """The verify layer at its real size: 4 candidates x 1560 tokens, each over
+    the shared 6240-token committed prefix (pool row 0 of a 7800-slot pool)
+    plus its own tokens, read-only cache, against the fp32 oracle."""
+    from wam_ops import synthetic
+    shape = synthetic.WAN22_5B
+    params = synthetic.block_params(shape, seed=2)
+    B, M, prefix = 4, 1560, 6240
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, B, M, (2, 26, 30), context_len=512, seed=3)
+    blk = native_block(params, shape, dev)
+    cache = synthetic.kv_pool(shape, prefix + M, prefix, batch=1, seed=4, device=dev)
+    blk.attn1.attn_caches["pos"] = cache
+    ocache = {k: (v.float().cpu() if v.dtype == torch.bfloat16 else v.cpu()) for k, v in cache.items()}
+    rows = torch.zeros(B, dtype=torch.int64)
+    with torch.no_grad():
+        out = blk(x.to(dev), ctx[:1].to(dev), temb.to(dev), freqs.to(dev), update_cache=0,
+                  candidate_cache_rows=rows.to(dev))
+    torch.cuda.synchronize()
+    ref = block_forward(params, x, ctx[:1], temb, freqs, shape.heads, shape.eps, cache=ocache, update_cache=0,
+                        candidate_rows=rows)
+    m = assert_close(out.cpu(), ref, max_abs=2e-2, min_cos=0.9999, what="verify layer 4x1560 over 6240")
+    assert torch.equal(blk.attn1.attn_caches["pos"]["mask"].cpu(), ocache["mask"])
+    print("verify parity", m)
+
+
 def test_block_debug_intermediates(dev):
     from wam_ops import synthetic
     shape = _shape(**TINY)
