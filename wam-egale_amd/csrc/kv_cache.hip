@@ -75,10 +75,15 @@ __device__ inline long long block_reduce_ll(long long v, bool take_max, long lon
   return r;
 }
 
+// Thread t owns the contiguous slots [t * S, t * S + S) (S = ceil(P / 1024)),
+// so every list below is built in ascending slot order by one block scan over
+// per-thread counts, and each thread issues the loads of its slots together.
 __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout_args a) {
   __shared__ int sh_i[kLayoutWaves];
   __shared__ long long sh_ll[kLayoutWaves];
   const int tid = threadIdx.x, P = a.pool;
+  const int S = (P + kLayoutThreads - 1) / kLayoutThreads;
+  const int lo = min(tid * S, P), hi = min(lo + S, P);
   int error = 0;
   if (a.candidate) {
     int bad = 0;
@@ -88,34 +93,29 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   } else {
     // Eviction of the oldest ids (allocate_slots).
     int nfree = 0;
-    for (int c = 0; c < P; c += kLayoutThreads) {
-      const int i = c + tid;
-      nfree += block_sum(i < P && !a.mask[i], sh_i);
-    }
-    int need = a.tokens - nfree;
+    for (int i = lo; i < hi; ++i) nfree += a.mask[i] ? 0 : 1;
+    int need = a.tokens - block_sum(nfree, sh_i);
     while (need > 0) {
       long long mn = 0x7fffffffffffffffLL;
-      for (int c = 0; c < P; c += kLayoutThreads) {
-        const int i = c + tid;
-        const long long v = (i < P && a.mask[i]) ? (long long)a.ids[i] : 0x7fffffffffffffffLL;
-        const long long r = block_reduce_ll(v, false, sh_ll);
-        mn = r < mn ? r : mn;
-      }
-      int base = 0;
-      for (int c = 0; c < P; c += kLayoutThreads) {
-        const int i = c + tid;
-        const int f = (i < P && a.mask[i] && a.ids[i] == mn) ? 1 : 0;
-        int tot;
-        const int pos = block_excl_scan(f, sh_i, &tot) + base;
-        if (f && pos < need) {
-          a.mask[i] = 0;
-          a.ids[i] = -1;
+      for (int i = lo; i < hi; ++i)
+        if (a.mask[i] && (long long)a.ids[i] < mn) mn = (long long)a.ids[i];
+      mn = block_reduce_ll(mn, false, sh_ll);
+      int f = 0;
+      for (int i = lo; i < hi; ++i) f += (a.mask[i] && a.ids[i] == mn) ? 1 : 0;
+      int tot;
+      int pos = block_excl_scan(f, sh_i, &tot);
+      for (int i = lo; i < hi; ++i) {
+        if (a.mask[i] && a.ids[i] == mn) {
+          if (pos < need) {
+            a.mask[i] = 0;
+            a.ids[i] = -1;
+          }
+          ++pos;
         }
-        base += tot;
       }
-      need -= base;
+      need -= tot;
       __syncthreads();
-      if (base == 0) {  // no valid slot left to evict: the host checks make this unreachable
+      if (tot == 0) {  // no valid slot left to evict: the host checks make this unreachable
         error = 1;
         break;
       }
@@ -124,35 +124,36 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   // Next id over the (post-eviction) valid slots (_next_cache_id).
   long long next = -1;
   if (!a.candidate) {
-    for (int c = 0; c < P; c += kLayoutThreads) {
-      const int i = c + tid;
-      const long long v = (i < P && a.mask[i]) ? (long long)a.ids[i] : -1LL;
-      const long long r = block_reduce_ll(v, true, sh_ll);
-      next = r > next ? r : next;
-    }
-    next += 1;
+    long long mx = -1;
+    for (int i = lo; i < hi; ++i)
+      if (a.mask[i] && (long long)a.ids[i] > mx) mx = (long long)a.ids[i];
+    next = block_reduce_ll(mx, true, sh_ll) + 1;
   }
   // History list and new slots, both in ascending slot order.
-  int base_v = 0, base_f = 0;
-  for (int c = 0; c < P; c += kLayoutThreads) {
-    const int i = c + tid;
-    const int valid = (i < P && a.mask[i]) ? 1 : 0;
-    const int fr = (!a.candidate && i < P && !valid) ? 1 : 0;
-    int tv, tf;
-    const int pv = block_excl_scan(valid, sh_i, &tv) + base_v;
-    const int pf = block_excl_scan(fr, sh_i, &tf) + base_f;
-    if (valid) a.hist_slots[pv] = i;
-    if (fr && pf < a.tokens) {
-      a.new_slots[pf] = i;
-      a.mask[i] = a.update != 0 ? 1 : 0;
-      a.ids[i] = next;
-      a.is_pred[i] = a.update == 1 ? 1 : 0;
+  int nv = 0, nf = 0;
+  for (int i = lo; i < hi; ++i) {
+    const int valid = a.mask[i] ? 1 : 0;
+    nv += valid;
+    nf += (!a.candidate && !valid) ? 1 : 0;
+  }
+  int tv, tf;
+  int pv = block_excl_scan(nv, sh_i, &tv);
+  int pf = block_excl_scan(nf, sh_i, &tf);
+  for (int i = lo; i < hi; ++i) {
+    const bool valid = a.mask[i];
+    if (valid) a.hist_slots[pv++] = i;
+    if (!a.candidate && !valid) {
+      if (pf < a.tokens) {
+        a.new_slots[pf] = i;
+        a.mask[i] = a.update != 0 ? 1 : 0;
+        a.ids[i] = next;
+        a.is_pred[i] = a.update == 1 ? 1 : 0;
+      }
+      ++pf;
     }
-    base_v += tv;
-    base_f += tf;
   }
   if (tid == 0) {
-    a.info[0] = base_v;
+    a.info[0] = tv;
     a.info[1] = error;
   }
 }
