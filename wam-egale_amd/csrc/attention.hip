@@ -86,6 +86,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   // Q fragments (B operand of S^T = K Q^T): query qi, d = 16 ks + 8 half .. +8.
   const int qi = qt * QT + wave * 32 + l32;
   const bool q_ok = qi < a.Mq;
+  const bool live = qt * QT + wave * 32 < a.Mq;  // wave-uniform
   const bf16* qp = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride +
                    (int64_t)(q_ok ? qi : 0) * a.q_rstride + h * kAttnHD + half * 8;
   bf16x8 qf[8];
@@ -162,6 +163,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
       __builtin_amdgcn_s_barrier();
       if (t + kAttnStages - 1 < ntiles)
         issue(t_first + t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages));
+      if (!live) continue;  // this wave's queries are all past Mq; it still loads and syncs
       const char* kb = WAM_ATTN_BUF(st);
       const char* vb = kb + kAttnTile;
 
@@ -333,13 +335,22 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
   *reinterpret_cast<bf16x2*>(op + 2 * lane) = r;
 }
 
-// Key-range splits for a query grid of `base` 256-query workgroups: enough to
-// give every CU about two workgroups, at most 8.
+// Key-range splits for a query grid of `base` 256-query workgroups, used when
+// that grid is under 1.5 waves of workgroups on 256 CUs.  Among 1..8 splits
+// the one with the fewest dispatch rounds per unit of work wins, each split
+// beyond the first charged 2.5% of a unit for its pipeline fill and its share
+// of the combine: 168 workgroups take 3 splits (2 rounds of thirds), 24 take 8.
 static int attention_splits(int B, int Mq, int H) {
   const int64_t base = (int64_t)((Mq + 255) / 256) * H * B;
   if (base >= 384 || base <= 0) return 1;
-  const int64_t ns = (512 + base - 1) / base;
-  return (int)(ns < 8 ? ns : 8);
+  constexpr int kCUs = 256;
+  int best = 1;
+  double best_cost = 1e30;
+  for (int ns = 1; ns <= 8; ++ns) {
+    const double cost = (double)((base * ns + kCUs - 1) / kCUs) / ns + 0.025 * (ns - 1);
+    if (cost < best_cost - 1e-9) best_cost = cost, best = ns;
+  }
+  return best;
 }
 
 int64_t attention_workspace_bytes(int B, int Mq, int H) {
