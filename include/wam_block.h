@@ -191,15 +191,17 @@ typedef struct {
   const void* k; const void* v; int64_t kv_bstride, kv_rstride; int Mk;
   const int64_t* kv_rows; int kv_batch;
   float scale;
-  /* Optional workspace for key-range splits (used when the query grid alone
-   * would leave CUs idle): at least wam_attention_workspace_bytes(B, Mq, H)
-   * bytes, or NULL to run unsplit.  Not in the reference (its FlashAttention
-   * call chooses splits internally). */
-  void* workspace; int64_t workspace_bytes;
+  /* Optional workspace for key-range splits of the last dispatch round
+   * (used when the query grid alone would leave CUs idle): at least
+   * wam_attention_workspace_bytes(B, Mq, H, max_keys) bytes, or NULL to run
+   * unsplit.  max_keys: host-side upper bound of Mk + n_hist (0 = Mk), used
+   * only to plan the split.  Not in the reference (its FlashAttention call
+   * chooses splits internally). */
+  void* workspace; int64_t workspace_bytes; int max_keys;
 } wam_attention_args;
 
 int wam_attention(const wam_attention_args* args, void* stream);
-int64_t wam_attention_workspace_bytes(int B, int Mq, int H);
+int64_t wam_attention_workspace_bytes(int B, int Mq, int H, int max_keys);
 
 /* ------------------------------------------------------------- KV pool */
 /* Device-side bookkeeping of the original-mode KV pool (model.py:547-593):

@@ -95,6 +95,24 @@ def test_workspace_size():
     expect = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
               + R * 4)  # new-slot list
     assert expect <= n < expect + 4096
+    # 4680 queries over their own 4680 keys fill two dispatch rounds: no split
+    assert h.wam_attention_workspace_bytes(1, R, 24, R) == 0
+
+
+def test_attention_split_plan_workspace():
+    h = _lib.lib()
+    # 4 x 1560 queries over 1560 own + 7800 pool keys: 512 whole units, the
+    # other 160 in 3 key ranges of fp32 partials (256 queries x (128 + 2)).
+    assert h.wam_attention_workspace_bytes(4, 1560, 24, 1560 + 7800) == 3 * 160 * 256 * 130 * 4
+    # one 1560-query chunk over 7800 keys: all 168 units in 3 ranges
+    assert h.wam_attention_workspace_bytes(1, 1560, 24, 7800) == 3 * 168 * 256 * 130 * 4
+    # short key lists are never split (cross attention over 512 text tokens)
+    assert h.wam_attention_workspace_bytes(4, 1560, 24, 512) == 0
+    # the block reserves the larger of its self and cross attention needs
+    R, D, F, Lc, P = 1560, 3072, 14336, 512, 7800
+    base = h.wam_block_workspace_bytes(4, R, D, F, 1, Lc, 0)
+    with_pool = h.wam_block_workspace_bytes(4, R, D, F, 1, Lc, P)
+    assert with_pool - base >= 3 * 160 * 256 * 130 * 4
 
 
 def test_modulation_host_validation():

@@ -176,7 +176,8 @@ def test_attention_strided_and_broadcast(dev):
 @pytest.mark.parametrize("B,Mq,P,nvalid,Bp,candidate", [(1, 50, 300, 170, 1, False),
                                                         (2, 64, 500, 321, 2, False),
                                                         (4, 33, 400, 250, 2, True),
-                                                        (4, 1560, 7800, 6240, 1, True)])
+                                                        (4, 1560, 7800, 6240, 1, True),
+                                                        (2, 1560, 7800, 5000, 2, False)])
 def test_attention_history(dev, B, Mq, P, nvalid, Bp, candidate):
     from wam_ops import ops
     H = 2 if Mq < 1000 else 24

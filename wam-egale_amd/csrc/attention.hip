@@ -43,13 +43,16 @@ __device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n -
 
 // Workgroup: W waves x 32 queries of one (batch row, head).  Wave w owns
 // queries q0 + 32 w .. +32 and keeps its Q fragments in registers.
-// n_split > 1: the key tiles of each (query tile, batch row, head) are split
-// into n_split contiguous ranges, one per workgroup; each writes its
-// unnormalised O and its (max, sum) to `part`, and attention_combine_kernel
-// merges them.  Used when the query grid alone would leave CUs idle.
+// A unit is one (query tile, batch row, head), numbered query tile fastest.
+// Workgroups 0 .. n_full-1 each run one whole unit (n_full = all units when
+// nothing is split).  Each of the remaining units is split into n_split
+// contiguous key ranges, one workgroup per range; those write their
+// unnormalised O and their (max, sum) to `part`, and attention_combine_kernel
+// merges them.  Whole units are dispatched first, so the splits fill the last
+// dispatch round evenly.
 template <int W>
 __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args a,
-                                                              const int* __restrict__ slots,
+                                                              const int* __restrict__ slots, int n_full,
                                                               int n_split, float* __restrict__ part) {
   // One __shared__ object per stage: the compiler tracks direct-to-LDS loads
   // per object, so reading one stage while others are being filled does not
@@ -67,9 +70,21 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   static_assert(16 % W == 0, "waves must divide the 16 K blocks of a stage");
 
   const int nqt = (a.Mq + QT - 1) / QT;
-  const int id = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
-  const int qt = id % nqt, rest = id / nqt;
-  const int split = rest % n_split, bh = rest / n_split;
+  const int n_tail = nqt * a.H * a.B - n_full;  // split units
+  int unit, split = 0, ns = 1;
+  if ((int)blockIdx.x < n_full) {
+    unit = xcd_remap(blockIdx.x, n_full);
+  } else {
+    // consecutive pieces: consecutive units of one key range (shared K/V in L2)
+    const int piece = xcd_remap(blockIdx.x - n_full, gridDim.x - n_full);
+    unit = n_full + piece % n_tail;
+    split = piece / n_tail;
+    ns = n_split;
+  }
+  unit = __builtin_amdgcn_readfirstlane(unit);
+  split = __builtin_amdgcn_readfirstlane(split);
+  ns = __builtin_amdgcn_readfirstlane(ns);
+  const int qt = unit % nqt, bh = unit / nqt;
   const int h = bh % a.H, b = bh / a.H;
 
   const int n_hist = a.n_hist_dev ? __builtin_amdgcn_readfirstlane(*a.n_hist_dev) : 0;
@@ -140,8 +155,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   // Key tiles [t_first, t_first + ntiles) of this workgroup's split; t below
   // counts from t_first.
   const int all_tiles = (n_tot + kAttnKT - 1) / kAttnKT;
-  const int t_first = (int)((int64_t)split * all_tiles / n_split);
-  const int ntiles = (int)((int64_t)(split + 1) * all_tiles / n_split) - t_first;
+  const int t_first = (int)((int64_t)split * all_tiles / ns);
+  const int ntiles = (int)((int64_t)(split + 1) * all_tiles / ns) - t_first;
 #pragma unroll
   for (int st = 0; st < kAttnStages - 1; ++st)
     if (st < ntiles) issue(t_first + st, WAM_ATTN_BUF(st));
@@ -269,11 +284,12 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 #undef WAM_ATTN_BUF
 
   const float l = l_run + __shfl_xor(l_run, 32, 64);
-  if (n_split > 1) {
-    // Partial result of this split: O (unnormalised, relative to m_run), and
-    // (m_run, l) of the query; an empty split leaves m = -inf, l = 0, O = 0.
+  if (ns > 1) {
+    // Partial result of this key range: O (unnormalised, relative to m_run),
+    // and (m_run, l) of the query; an empty range leaves m = -inf, l = 0,
+    // O = 0.  Row (split, split unit, query in tile).
     if (q_ok) {
-      const int64_t row = (((int64_t)split * a.B + b) * a.Mq + qi) * a.H + h;
+      const int64_t row = ((int64_t)split * n_tail + (unit - n_full)) * QT + wave * 32 + l32;
       float* op = part + row * kAttnHD;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
@@ -282,7 +298,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
           *reinterpret_cast<float4*>(op + dt * 32 + 8 * g + 4 * half) =
               make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
       if (half == 0) {
-        float* ml = part + (int64_t)n_split * a.B * a.Mq * a.H * kAttnHD + row * 2;
+        float* ml = part + (int64_t)n_split * n_tail * QT * kAttnHD + row * 2;
         *reinterpret_cast<float2*>(ml) = make_float2(m_run, l);
       }
     }
@@ -303,30 +319,48 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   }
 }
 
-// Merge the n_split partial results of one (batch row, query, head) row:
+// Merge the n_split partial results of each query row of the split units:
 // O = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with m = max_i m_i.  One
-// wave per row, two of the 128 outputs per lane.
-__global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_args a, int n_split,
+// wave per (split unit, query) row, two of the 128 outputs per lane; every
+// range's loads are issued before any of them is used.
+constexpr int kAttnSplitQT = 256;  // the split path runs the 8-wave kernel
+constexpr int kAttnMaxSplit = 8;
+__global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_args a, int n_full, int n_split,
                                                                 const float* __restrict__ part) {
+  constexpr int QT = kAttnSplitQT;
   const int lane = threadIdx.x & 63;
-  const int64_t rows = (int64_t)a.B * a.Mq * a.H;
+  const int nqt = (a.Mq + QT - 1) / QT;
+  const int n_tail = nqt * a.H * a.B - n_full;
+  const int64_t rows = (int64_t)n_tail * QT;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
+  const int unit = n_full + (int)(row / QT), qq = (int)(row % QT);
+  const int qt = unit % nqt, bh = unit / nqt;
+  const int qi = qt * QT + qq;
+  if (qi >= a.Mq) return;
+  const int h = bh % a.H, b = bh / a.H;
   const float* ml = part + (int64_t)n_split * rows * kAttnHD;
-  float m = -INFINITY;
-  for (int i = 0; i < n_split; ++i) m = fmaxf(m, ml[((int64_t)i * rows + row) * 2]);
-  float den = 0.f, n0 = 0.f, n1 = 0.f;
-  for (int i = 0; i < n_split; ++i) {
-    const float mi = ml[((int64_t)i * rows + row) * 2];
-    const float w = mi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mi - m);
-    den += w * ml[((int64_t)i * rows + row) * 2 + 1];
-    const float2 v = *reinterpret_cast<const float2*>(part + ((int64_t)i * rows + row) * kAttnHD + 2 * lane);
-    n0 += w * v.x;
-    n1 += w * v.y;
+  float2 mlv[kAttnMaxSplit], ov[kAttnMaxSplit];
+#pragma unroll
+  for (int i = 0; i < kAttnMaxSplit; ++i) {
+    mlv[i] = make_float2(-INFINITY, 0.f);
+    ov[i] = make_float2(0.f, 0.f);
+    if (i < n_split) {
+      mlv[i] = *reinterpret_cast<const float2*>(ml + ((int64_t)i * rows + row) * 2);
+      ov[i] = *reinterpret_cast<const float2*>(part + ((int64_t)i * rows + row) * kAttnHD + 2 * lane);
+    }
   }
-  const int h = (int)(row % a.H);
-  const int64_t bq = row / a.H;
-  const int qi = (int)(bq % a.Mq), b = (int)(bq / a.Mq);
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kAttnMaxSplit; ++i) m = fmaxf(m, mlv[i].x);
+  float den = 0.f, n0 = 0.f, n1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kAttnMaxSplit; ++i) {
+    const float w = mlv[i].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mlv[i].x - m);
+    den += w * mlv[i].y;
+    n0 += w * ov[i].x;
+    n1 += w * ov[i].y;
+  }
   bf16* op = static_cast<bf16*>(a.o) + (int64_t)b * a.o_bstride + (int64_t)qi * a.o_rstride + h * kAttnHD;
   const float inv = 1.f / den;
   bf16x2 r;
@@ -335,27 +369,54 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
   *reinterpret_cast<bf16x2*>(op + 2 * lane) = r;
 }
 
-// Key-range splits for a query grid of `base` 256-query workgroups, used when
-// that grid is under 1.5 waves of workgroups on 256 CUs.  Among 1..8 splits
-// the one with the fewest dispatch rounds per unit of work wins, each split
-// beyond the first charged 2.5% of a unit for its pipeline fill and its share
-// of the combine: 168 workgroups take 3 splits (2 rounds of thirds), 24 take 8.
-static int attention_splits(int B, int Mq, int H) {
-  const int64_t base = (int64_t)((Mq + 255) / 256) * H * B;
-  if (base >= 384 || base <= 0) return 1;
-  constexpr int kCUs = 256;
-  int best = 1;
-  double best_cost = 1e30;
-  for (int ns = 1; ns <= 8; ++ns) {
-    const double cost = (double)((base * ns + kCUs - 1) / kCUs) / ns + 0.025 * (ns - 1);
-    if (cost < best_cost - 1e-9) best_cost = cost, best = ns;
+// Launch plan of the split path: the first n_full units run whole, the other
+// n_tail units are split into n_split key ranges each.  Cost model, in units
+// of one whole unit's run time on one CU (kt key tiles of 64 keys), for 256
+// CUs taking workgroups in dispatch order:
+//   n_full / 256  +  ceil(pieces / 256) * (1 / n_split + kFill / kt)
+//                 +  pieces * kCombine / kt,         pieces = n_tail * n_split
+// kFill: key tiles' worth of pipeline fill and partial-result store per
+// piece; kCombine: the combine's time per piece (a 133 KB fp32 partial at
+// about 4 TB/s, ~33 ns) in key-tile times (~2.5 us per tile and CU).  The plan
+// with the lowest cost whose partials fit in max_bytes wins; no split when
+// none beats the whole-unit grid.  E.g. 4 x 1560 queries over 7800 keys (672
+// units, kt 122): 512 whole + 160 units in 3 ranges, 2.74 vs 3 rounds.
+struct AttnPlan {
+  int n_full, n_split, n_tail;
+};
+constexpr int kPlanCUs = 256;
+constexpr int64_t kPartBytesPerPiece = (int64_t)kAttnSplitQT * (kAttnHD + 2) * 4;
+
+static int64_t plan_bytes(const AttnPlan& p) {
+  return p.n_split > 1 ? (int64_t)p.n_split * p.n_tail * kPartBytesPerPiece : 0;
+}
+
+static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_bytes) {
+  constexpr double kFill = 1.5, kCombine = 0.0133;
+  const int64_t units = (int64_t)((Mq + kAttnSplitQT - 1) / kAttnSplitQT) * H * B;
+  AttnPlan best{(int)units, 1, 0};
+  if (units <= 0 || units >= (1 << 26)) return best;
+  const double kt = (double)((keys > 0 ? keys : 1) + kAttnKT - 1) / kAttnKT;
+  double best_cost = (double)((units + kPlanCUs - 1) / kPlanCUs);
+  for (int64_t F = 0; F < units; F += kPlanCUs) {
+    const int64_t T = units - F;
+    for (int ns = 2; ns <= kAttnMaxSplit; ++ns) {
+      const int64_t pieces = T * ns;
+      if (pieces * kPartBytesPerPiece > max_bytes) break;
+      const double cost = (double)F / kPlanCUs +
+                          (double)((pieces + kPlanCUs - 1) / kPlanCUs) * (1.0 / ns + kFill / kt) +
+                          (double)pieces * kCombine / kt;
+      if (cost < best_cost - 1e-9) {
+        best_cost = cost;
+        best = AttnPlan{(int)F, ns, (int)T};
+      }
+    }
   }
   return best;
 }
 
-int64_t attention_workspace_bytes(int B, int Mq, int H) {
-  const int ns = attention_splits(B, Mq, H);
-  return ns > 1 ? (int64_t)ns * B * Mq * H * (kAttnHD + 2) * 4 : 0;
+int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
+  return plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX));
 }
 
 int attention(const wam_attention_args* a, hipStream_t s) {
@@ -381,29 +442,34 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   if (!a->kv_rows)
     WAM_REQUIRE(a->B <= a->kv_batch || a->kv_batch == 1,
                 "wam_attention: B=%d exceeds kv batch %d", a->B, a->kv_batch);
+  WAM_REQUIRE(a->max_keys >= 0, "wam_attention: max_keys must be >= 0");
   if (a->Mq == 0) return WAM_OK;
-  // 8 waves (256 queries) per workgroup when that still fills the chip;
-  // otherwise key-range splits (when the caller gave a workspace for the
-  // partial results), else 4-wave workgroups.
+  // 8 waves (256 queries) per workgroup, with the last dispatch round split
+  // by key ranges when the plan says so and the caller gave a workspace for
+  // the partial results; small unsplit grids use 4-wave workgroups.
   const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
   WAM_REQUIRE(grid8 < (1 << 26), "wam_attention: grid too large");
-  const int ns = attention_splits(a->B, a->Mq, a->H);
-  if (ns > 1 && a->workspace && a->workspace_bytes >= attention_workspace_bytes(a->B, a->Mq, a->H)) {
+  const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
+  const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0);
+  if (p.n_split > 1) {
     float* part = static_cast<float*>(a->workspace);
-    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)(grid8 * ns)), dim3(512), 0, s, *a, a->slots, ns,
-                       part);
+    const int64_t grid = (int64_t)p.n_full + (int64_t)p.n_tail * p.n_split;
+    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full,
+                       p.n_split, part);
     WAM_LAUNCHED("attention_kernel");
-    const int64_t rows = (int64_t)a->B * a->Mq * a->H;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, *a, ns,
-                       static_cast<const float*>(part));
+    const int64_t rows = (int64_t)p.n_tail * kAttnSplitQT;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, *a,
+                       p.n_full, p.n_split, static_cast<const float*>(part));
     WAM_LAUNCHED("attention_combine_kernel");
     return WAM_OK;
   }
   if (grid8 >= 256) {
-    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, 1, nullptr);
+    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1,
+                       nullptr);
   } else {
     const int64_t grid4 = (int64_t)((a->Mq + 127) / 128) * a->H * a->B;
-    hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid4), dim3(256), 0, s, *a, a->slots, 1, nullptr);
+    hipLaunchKernelGGL(attention_kernel<4>, dim3((unsigned)grid4), dim3(256), 0, s, *a, a->slots, (int)grid4, 1,
+                       nullptr);
   }
   WAM_LAUNCHED("attention_kernel");
   return WAM_OK;
@@ -415,6 +481,6 @@ extern "C" int wam_attention(const wam_attention_args* args, void* stream) {
   return wam::attention(args, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int64_t wam_attention_workspace_bytes(int B, int Mq, int H) {
-  return wam::attention_workspace_bytes(B, Mq, H);
+extern "C" int64_t wam_attention_workspace_bytes(int B, int Mq, int H, int max_keys) {
+  return wam::attention_workspace_bytes(B, Mq, H, max_keys);
 }

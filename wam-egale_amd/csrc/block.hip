@@ -30,7 +30,7 @@ int linear(const wam_linear_args*, hipStream_t);
 int ln_modulate(const wam_ln_args*, hipStream_t);
 int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
-int64_t attention_workspace_bytes(int B, int Mq, int H);
+int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys);
 int kv_layout(const wam_kv_layout_args*, hipStream_t);
 int kv_commit(const wam_kv_commit_args*, hipStream_t);
 
@@ -88,8 +88,11 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   L.slots = take((size_t)(pool > 0 ? pool : 1) * 4);
   L.newslots = take((size_t)(M > 0 ? M : 1) * 4);
   L.info = take(16);
-  // key-range split partials of the self and cross attention (same query grid)
-  L.attnws_bytes = (size_t)attention_workspace_bytes(B, M, D / 128);
+  // key-range split partials of the self attention (own keys + the pool) and
+  // the cross attention (context keys); the two share one region
+  const int64_t ws_self = attention_workspace_bytes(B, M, D / 128, (int64_t)M + (pool > 0 ? pool : 0));
+  const int64_t ws_cross = attention_workspace_bytes(B, M, D / 128, Lc);
+  L.attnws_bytes = (size_t)(ws_self > ws_cross ? ws_self : ws_cross);
   L.attnws = take(L.attnws_bytes);
   L.total = off;
   return L;
@@ -258,6 +261,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     }
     t.k = qkv + D; t.v = qkv + 2 * D; t.kv_bstride = (int64_t)M * 3 * D; t.kv_rstride = 3 * D;
     t.Mk = M; t.kv_batch = B;
+    t.max_keys = M + (cache ? a->pool : 0);
     t.scale = 1.0f / sqrtf((float)W->head_dim);
     t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
     WAM_TRY(attention(&t, s));
@@ -333,6 +337,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.k = ck; t.v = cv; t.kv_bstride = (int64_t)a->context_len * D; t.kv_rstride = D;
     t.Mk = a->context_len; t.kv_batch = a->context_batch;
     t.kv_rows = a->context_rows;
+    t.max_keys = a->context_len;
     t.scale = 1.0f / sqrtf((float)W->head_dim);
     t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
     WAM_TRY(attention(&t, s));

@@ -65,7 +65,7 @@ class AttentionArgs(Structure):
                 ("n_hist_dev", c_void_p), ("pool_rows", c_void_p), ("k", c_void_p),
                 ("v", c_void_p), ("kv_bstride", c_int64), ("kv_rstride", c_int64),
                 ("Mk", c_int), ("kv_rows", c_void_p), ("kv_batch", c_int), ("scale", c_float),
-                ("workspace", c_void_p), ("workspace_bytes", c_int64)]
+                ("workspace", c_void_p), ("workspace_bytes", c_int64), ("max_keys", c_int)]
 
 
 class KvLayoutArgs(Structure):
@@ -135,7 +135,7 @@ STRUCTS = {
 # Every symbol include/wam_block.h declares, with its ctypes signature.
 SIGNATURES = {
     "wam_linear": (c_int, [POINTER(LinearArgs), c_void_p]),
-    "wam_attention_workspace_bytes": (c_int64, [c_int, c_int, c_int]),
+    "wam_attention_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "wam_quantize_fp8_rows": (c_int, [c_void_p, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
     "wam_ln_modulate": (c_int, [POINTER(LnArgs), c_void_p]),
     "wam_rms_rope": (c_int, [POINTER(RmsRopeArgs), c_void_p]),

@@ -270,10 +270,12 @@ def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, poo
         _req(kv_rows.dtype == torch.int64 and kv_rows.numel() == B, "kv_rows int64 [B]")
         a.kv_rows = kv_rows.data_ptr()
     a.scale = scale if scale is not None else 1.0 / math.sqrt(hd)
+    # the key count bound plans the split: own keys plus the whole pool
+    a.max_keys = a.Mk + (pool_k.shape[1] if n_hist is not None else 0)
     ws = None
-    nbytes = _lib.lib().wam_attention_workspace_bytes(a.B, a.Mq, a.H)
+    nbytes = _lib.lib().wam_attention_workspace_bytes(a.B, a.Mq, a.H, a.max_keys)
     if nbytes > 0:
-        # partial results of key-range splits (small query grids)
+        # partial results of the key-range splits
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
     _lib.check(_lib.lib().wam_attention(ctypes.byref(a), stream_handle(dev)), "wam_attention")
