@@ -129,9 +129,16 @@ typedef struct {
    * no fp8 path. */
   int w_dtype;
   const float* w_scale[3];
+  /* Optional workspace for the split-K tail: when the 256x256 tiles leave
+   * a partial last round, the remaining output columns may run split over k
+   * with fp32 partial sums here (at least wam_linear_workspace_bytes(M,
+   * seg_n, n_seg, K) bytes), or, without it, as smaller tiles.  Not in the
+   * reference (cuBLASLt picks its own algorithm and workspace). */
+  void* workspace; int64_t workspace_bytes;
 } wam_linear_args;
 
 int wam_linear(const wam_linear_args* args, void* stream);
+int64_t wam_linear_workspace_bytes(int M, int N, int n_seg, int K);
 
 /* Per-row fp8 quantization of a bf16 matrix w [rows, cols] (row stride ldw):
  * scale[r] = max_c |w[r,c]| / 448 (1 for an all-zero row) and

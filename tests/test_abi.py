@@ -99,6 +99,22 @@ def test_workspace_size():
     assert h.wam_attention_workspace_bytes(1, R, 24, R) == 0
 
 
+def test_linear_split_k_plan_workspace():
+    h = _lib.lib()
+    # 6240 x 14336 -> 3072 (FFN2 of 4 x 1560 rows): 250 whole 256x256 tiles,
+    # the last 2 tile columns (50 tiles) in 5 k ranges of fp32 partials
+    assert h.wam_linear_workspace_bytes(6240, 3072, 1, 14336) == 5 * 6240 * 512 * 4
+    # 6240 x 3072 -> 14336 (FFN1): 1275 whole tiles, 125 tail tiles in 2 ranges
+    assert h.wam_linear_workspace_bytes(6240, 14336, 1, 3072) == 2 * 6240 * 1280 * 4
+    assert h.wam_linear_workspace_bytes(6240, 2816, 1, 3072) == 8 * 6240 * 256 * 4
+    # short k (3072 -> 3072) keeps the 128x128 tail; 4680 rows leave no
+    # partial round worth splitting; QKV (three segments) is never split
+    assert h.wam_linear_workspace_bytes(6240, 3072, 1, 3072) == 0
+    assert h.wam_linear_workspace_bytes(4680, 14336, 1, 3072) == 0
+    assert h.wam_linear_workspace_bytes(4680, 3072, 1, 14336) == 0
+    assert h.wam_linear_workspace_bytes(6240, 3072, 3, 3072) == 0
+
+
 def test_attention_split_plan_workspace():
     h = _lib.lib()
     # 4 x 1560 queries over 1560 own + 7800 pool keys: 512 whole units, the
@@ -108,11 +124,16 @@ def test_attention_split_plan_workspace():
     assert h.wam_attention_workspace_bytes(1, 1560, 24, 7800) == 3 * 168 * 256 * 130 * 4
     # short key lists are never split (cross attention over 512 text tokens)
     assert h.wam_attention_workspace_bytes(4, 1560, 24, 512) == 0
-    # the block reserves the larger of its self and cross attention needs
-    R, D, F, Lc, P = 1560, 3072, 14336, 512, 7800
-    base = h.wam_block_workspace_bytes(4, R, D, F, 1, Lc, 0)
-    with_pool = h.wam_block_workspace_bytes(4, R, D, F, 1, Lc, P)
-    assert with_pool - base >= 3 * 160 * 256 * 130 * 4
+    # the block reserves one region for the largest of its split needs
+    B, M, D, F, Lc, P = 4, 1560, 3072, 14336, 512, 7800
+    R = B * M
+    core = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
+            + P * 4 + M * 4)  # slot lists
+    need = max(h.wam_attention_workspace_bytes(B, M, 24, M + P), h.wam_linear_workspace_bytes(R, D, 1, F),
+               h.wam_linear_workspace_bytes(R, F, 1, D))
+    assert need > 0
+    n = h.wam_block_workspace_bytes(B, M, D, F, 1, Lc, P)
+    assert core + need <= n < core + need + 4096
 
 
 def test_modulation_host_validation():

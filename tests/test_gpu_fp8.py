@@ -48,7 +48,10 @@ def test_quantize_rows_bit_exact(dev):
     assert torch.equal(q2.cpu().view(torch.uint8), qr2.view(torch.uint8)) and torch.equal(s2.cpu(), sr2)
 
 
-@pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 256, 3584), (4680, 512, 14336)])
+# (6240, 3072, 2816): 275 256x256 tiles; the last column of tiles runs split
+# over k in 8 ranges (fp32 partials, reduce pass with scale + epilogue).
+@pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 256, 3584), (4680, 512, 14336),
+                                   (6240, 3072, 2816)])
 def test_fp8_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     x = _randn((M, K), dev, 3)

@@ -51,9 +51,11 @@ def test_linear_bias(dev, M, K, N, nseg):
 # (4680, 256, 3584) and (4680, 256, 14336) have 266 and 1064 256x256 tiles:
 # just above a multiple of the 256 CUs, so their last columns run as a second
 # 128x128-tile launch (column offsets into bias, residual, output and the
-# modulation table).
+# modulation table).  (6240, 3072, 2816) and (6240, 6144, 3072) run their last
+# columns split over k (8 and 5 ranges of fp32 partials, then a reduce pass
+# with the epilogue).
 @pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
-                                   (4680, 256, 14336)])
+                                   (4680, 256, 14336), (6240, 3072, 2816), (6240, 6144, 3072)])
 def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     D = N

@@ -31,6 +31,7 @@ int ln_modulate(const wam_ln_args*, hipStream_t);
 int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
 int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys);
+int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K);
 int kv_layout(const wam_kv_layout_args*, hipStream_t);
 int kv_commit(const wam_kv_commit_args*, hipStream_t);
 
@@ -69,7 +70,7 @@ struct Scope {
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct Layout {
-  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, attnws, attnws_bytes, total;
+  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, split, split_bytes, total;
 };
 
 static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
@@ -88,12 +89,18 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   L.slots = take((size_t)(pool > 0 ? pool : 1) * 4);
   L.newslots = take((size_t)(M > 0 ? M : 1) * 4);
   L.info = take(16);
-  // key-range split partials of the self attention (own keys + the pool) and
-  // the cross attention (context keys); the two share one region
-  const int64_t ws_self = attention_workspace_bytes(B, M, D / 128, (int64_t)M + (pool > 0 ? pool : 0));
-  const int64_t ws_cross = attention_workspace_bytes(B, M, D / 128, Lc);
-  L.attnws_bytes = (size_t)(ws_self > ws_cross ? ws_self : ws_cross);
-  L.attnws = take(L.attnws_bytes);
+  // Partial results of the self attention's key-range splits (own keys + the
+  // pool), the cross attention's (context keys) and the split-K GEMM tails.
+  // One region: the kernels that use it run one after another on the stream.
+  const int64_t need[] = {attention_workspace_bytes(B, M, D / 128, (int64_t)M + (pool > 0 ? pool : 0)),
+                          attention_workspace_bytes(B, M, D / 128, Lc),
+                          linear_workspace_bytes((int)R, D, 1, D),   // self_out, cross_q, cross_out
+                          linear_workspace_bytes((int)R, F, 1, D),   // FFN1
+                          linear_workspace_bytes((int)R, D, 1, F)};  // FFN2
+  int64_t most = 0;
+  for (int64_t n : need) most = n > most ? n : most;
+  L.split_bytes = (size_t)most;
+  L.split = take(L.split_bytes);
   L.total = off;
   return L;
 }
@@ -187,6 +194,8 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
               "block: workspace of %zu bytes is smaller than the %zu required",
               a->workspace_bytes, L.total);
   char* ws = static_cast<char*>(a->workspace);
+  void* split_ws = L.split_bytes ? ws + L.split : nullptr;
+  const int64_t split_bytes = (int64_t)L.split_bytes;
   bf16* h = reinterpret_cast<bf16*>(ws + L.h);
   bf16* qkv = reinterpret_cast<bf16*>(ws + L.qkv);
   bf16* attn = reinterpret_cast<bf16*>(ws + L.attn);
@@ -219,6 +228,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.n_seg = 3;
     g.w[1] = W->w[5]; g.bias[1] = W->w[6]; g.out[1] = qkv + D;
     g.w[2] = W->w[7]; g.bias[2] = W->w[8]; g.out[2] = qkv + 2 * D;
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
   // 3. q/k RMSNorm across heads + RoPE, in place.
@@ -263,7 +273,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.Mk = M; t.kv_batch = B;
     t.max_keys = M + (cache ? a->pool : 0);
     t.scale = 1.0f / sqrtf((float)W->head_dim);
-    t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
+    t.workspace = L.split_bytes ? ws + L.split : nullptr; t.workspace_bytes = (int64_t)L.split_bytes;
     WAM_TRY(attention(&t, s));
   }
   WAM_TRY(copy_debug(a->debug, 4, attn, rowb, s));
@@ -284,6 +294,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     gemm_args(g, attn, D, R, D, D, W->w[9], W->w[10], x1, D);
     g.epilogue = WAM_EPI_BIAS_GATE_RES; g.res = a->x; g.ldr = D; g.gate = mod; g.gate_index = 2;
     g.out_dtype = WAM_F32;
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 5, x1, rowb * 2, s));
@@ -308,6 +319,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     Scope sc(a->timer, WAM_STAGE_CROSS_Q, s);
     wam_linear_args g;
     gemm_args(g, n2, D, R, D, D, W->w[13], W->w[14], cq, D);
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
     wam_rms_rope_args r{};
     r.x[0] = cq; r.y[0] = cq; r.gamma[0] = W->w[21]; r.eps[0] = W->eps[5];
@@ -339,7 +351,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.kv_rows = a->context_rows;
     t.max_keys = a->context_len;
     t.scale = 1.0f / sqrtf((float)W->head_dim);
-    t.workspace = L.attnws_bytes ? ws + L.attnws : nullptr; t.workspace_bytes = (int64_t)L.attnws_bytes;
+    t.workspace = L.split_bytes ? ws + L.split : nullptr; t.workspace_bytes = (int64_t)L.split_bytes;
     WAM_TRY(attention(&t, s));
   }
   WAM_TRY(copy_debug(a->debug, 10, attn, rowb, s));
@@ -350,6 +362,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     gemm_args(g, attn, D, R, D, D, W->w[19], W->w[20], x2, D);
     g.epilogue = WAM_EPI_BIAS_RES; g.res = x1; g.ldr = D; g.res_dtype = WAM_F32;
     g.out_dtype = WAM_F32;
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 11, x2, rowb * 2, s));
@@ -371,6 +384,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     if (W->ffn_fp8[0]) {
       g.w[0] = W->ffn_fp8[0]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[0];
     }
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 13, act, (size_t)R * F * 2, s));
@@ -384,6 +398,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
       g.w[0] = W->ffn_fp8[1]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[1];
     }
     g.gate = mod; g.gate_index = 5;
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 14, a->out, rowb, s));

@@ -31,7 +31,14 @@ struct LinearParams {
   const float* wscale[3];  // per-output-column fp32 scales of fp8 weights (else unused)
   int mod_d;   // row length of the modulation table (the full output width)
   int n_off;   // column of this launch's first output column in that table
+  // Split-K launches (one segment): k range kp of k_split writes its raw fp32
+  // sums to part[kp][m][n] (row stride seg_n); gemm_splitk_reduce_kernel adds
+  // the ranges in order and applies the epilogue.
+  int k_split;
+  float* part;
 };
+
+constexpr int kEpiPartial = 100;  // kernel epilogue of a split-K range: raw fp32 sums
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0,
           int WB_ = 2, int SPLIT_ = 1>
@@ -158,6 +165,50 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
   }
 }
 
+// The epilogue of 4 consecutive outputs (m, n..n+3) from their fp32 sums v:
+// fp8 column scale, bias, then GELU-tanh, or the (gated) residual with an
+// fp32 or bf16 output.
+template <int EPI, int WB>
+__device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int m, int n, const f32x4 v,
+                                          const float (&bv)[4], const float (&wsc)[4]) {
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
+  if constexpr (EPI == WAM_EPI_BIAS_GELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
+  } else if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
+    float rv[4];
+    const int64_t ro = (int64_t)m * p.ldr + n;
+    if (p.res_f32) {
+      const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
+      rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
+    } else {
+      const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
+    }
+    if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+      float gt[4];
+      ld_mod4(p.gate, p.mod_d, m, p.gate_index, n + p.n_off, gt);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
+    }
+    if (p.out_f32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * p.ldo + n) =
+          make_float4(y[0], y[1], y[2], y[3]);
+      return;
+    }
+  }
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
+  *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = o;
+}
+
 template <class C, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(LinearParams p) {
   // One __shared__ object per pipeline stage: the compiler tracks the
@@ -176,7 +227,13 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 
   // Tile order: XCD-contiguous ranges, then groups of 8 m-tiles swept along n
   // so that one XCD's L2 holds a few A row-panels and W column-panels.
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int kp = 0;  // k range of a split-K launch: pieces are (k range, tile), tiles fastest
+  if constexpr (EPI == kEpiPartial) {
+    const int tiles = p.m_tiles * p.n_tiles;
+    kp = __builtin_amdgcn_readfirstlane(tile / tiles);
+    tile -= kp * tiles;
+  }
   constexpr int G = 8;
   const int per_group = G * p.n_tiles;
   const int group = tile / per_group, in_group = tile - group * per_group;
@@ -198,11 +255,19 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // which is physical chunk L % KCH of row L / KCH, so it fetches the logical
   // chunk that the swizzle maps there.  Rows of A past M fall outside the
   // buffer resource and load as zeros.
+  // A split-K range starts kb k-tiles in: both resources start there, and
+  // their byte bounds shrink by the same amount.
+  int nk = p.K / C::BK, kb = 0;
+  if constexpr (EPI == kEpiPartial) {
+    kb = (int)((int64_t)kp * nk / p.k_split);
+    nk = (int)((int64_t)(kp + 1) * nk / p.k_split) - kb;
+  }
+  const uint32_t ka = (uint32_t)kb * C::BK * 2u, kw = (uint32_t)kb * C::BK * C::WB;
   const uint32_t a_bytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u;
-  const i32x4 ra = make_rsrc4(A + (int64_t)m0 * p.lda, a_bytes);
+  const i32x4 ra = make_rsrc4(A + (int64_t)m0 * p.lda + (int64_t)kb * C::BK, a_bytes - ka);
   // Weight rows past N (a partial last n-tile) load as zeros.
   const int n_rows = min(C::BN, p.seg_n - n0);
-  const i32x4 rb = make_rsrc4(W, (uint32_t)((int64_t)n_rows * p.ldw * C::WB));
+  const i32x4 rb = make_rsrc4(W + kw, (uint32_t)((int64_t)n_rows * p.ldw * C::WB) - kw);
   const int lrow = lane / C::KCH, pchunk = lane % C::KCH;
   // The swizzle term of row r = ROWS_PER_LOAD * g + lrow: for 128-byte rows
   // (8 rows per block) it depends on the parity of g, for 64-byte rows (16
@@ -230,7 +295,6 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) acc[j][i] = f32x16{};
 
-  const int nk = p.K / C::BK;
   const int half = lane >> 5, l32 = lane & 31;
   constexpr int KSTEPS = C::BK / 16;
   constexpr int MF = C::TM * C::TN, R = C::TM + C::TN;
@@ -372,42 +436,11 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       const int obj = rr / RPO, lr = rr % RPO;
       const char* buf = WAM_GEMM_BUF(obj);
       const f32x4 v = *reinterpret_cast<const f32x4*>(buf + lr * ROW_B + ((q ^ (lr & 15)) << 4));
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = C::WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
-      if constexpr (EPI == WAM_EPI_BIAS_GELU) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
-      } else if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
-        float rv[4];
-        const int64_t ro = (int64_t)m * p.ldr + n;
-        if (p.res_f32) {
-          const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
-          rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
-        } else {
-          const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
-        }
-        if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-          float gt[4];
-          ld_mod4(p.gate, p.mod_d, m, p.gate_index, n + p.n_off, gt);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
-        }
-        if (p.out_f32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(out) + (int64_t)m * p.ldo + n) =
-              make_float4(y[0], y[1], y[2], y[3]);
-          continue;
-        }
+      if constexpr (EPI == kEpiPartial) {
+        *reinterpret_cast<f32x4*>(p.part + ((int64_t)kp * p.M + m) * p.seg_n + n) = v;
+      } else {
+        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc);
       }
-      bf16x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
-      *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = o;
     }
     if (rd + 1 < NROUNDS) __syncthreads();
   }
@@ -428,6 +461,30 @@ using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 3, 1, 2, 1, 3>;
 using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
 using Cfg256x256k32w8t4s2 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2, 2, 2>;
 
+// Sum of the k_split fp32 partial ranges of a split-K launch (in range
+// order), then the launch's epilogue.  One thread per 4 consecutive outputs.
+template <int EPI, int WB>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p) {
+  const int q4 = p.seg_n / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.M * q4) return;
+  const int m = (int)(i / q4), n = (int)(i - (int64_t)m * q4) * 4;
+  const int64_t plane = (int64_t)p.M * p.seg_n, at = (int64_t)m * p.seg_n + n;
+  f32x4 v = *reinterpret_cast<const f32x4*>(p.part + at);
+  for (int r = 1; r < p.k_split; ++r) v += *reinterpret_cast<const f32x4*>(p.part + r * plane + at);
+  float bv[4] = {0.f, 0.f, 0.f, 0.f}, wsc[4] = {1.f, 1.f, 1.f, 1.f};
+  if (p.bias[0]) {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(p.bias[0] + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
+  }
+  if constexpr (WB == 1) {
+    const float4 t = *reinterpret_cast<const float4*>(p.wscale[0] + n);
+    wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
+  }
+  epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc);
+}
+
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
   WAM_REQUIRE(p.K % C::BK == 0 && (p.n_seg_count == 1 || p.seg_n % C::BN == 0),
@@ -436,6 +493,31 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
   p.m_tiles = (p.M + C::BM - 1) / C::BM;
   p.n_tiles = p.n_tiles_per_seg * p.n_seg_count;
   const int grid = p.m_tiles * p.n_tiles;
+  if (p.k_split > 1) {
+    WAM_REQUIRE(p.n_seg_count == 1 && p.part && p.k_split <= p.K / C::BK, "wam_linear: bad split-K launch");
+    hipLaunchKernelGGL((gemm_bf16_kernel<C, kEpiPartial>), dim3(grid * p.k_split), dim3(C::kThreads), 0, s, p);
+    WAM_LAUNCHED("gemm_bf16_kernel");
+    const unsigned rblocks = (unsigned)(((int64_t)p.M * (p.seg_n / 4) + 255) / 256);
+    switch (p.epi) {
+      case WAM_EPI_BIAS:
+        hipLaunchKernelGGL((gemm_splitk_reduce_kernel<WAM_EPI_BIAS, C::WB>), dim3(rblocks), dim3(256), 0, s, p);
+        break;
+      case WAM_EPI_BIAS_GELU:
+        hipLaunchKernelGGL((gemm_splitk_reduce_kernel<WAM_EPI_BIAS_GELU, C::WB>), dim3(rblocks), dim3(256), 0, s,
+                           p);
+        break;
+      case WAM_EPI_BIAS_GATE_RES:
+        hipLaunchKernelGGL((gemm_splitk_reduce_kernel<WAM_EPI_BIAS_GATE_RES, C::WB>), dim3(rblocks), dim3(256), 0,
+                           s, p);
+        break;
+      default:
+        hipLaunchKernelGGL((gemm_splitk_reduce_kernel<WAM_EPI_BIAS_RES, C::WB>), dim3(rblocks), dim3(256), 0, s,
+                           p);
+        break;
+    }
+    WAM_LAUNCHED("gemm_splitk_reduce_kernel");
+    return WAM_OK;
+  }
   switch (p.epi) {
     case WAM_EPI_BIAS:
       hipLaunchKernelGGL((gemm_bf16_kernel<C, WAM_EPI_BIAS>), dim3(grid), dim3(C::kThreads), 0, s, p);
@@ -482,36 +564,89 @@ static int cu_count() {
 }
 
 // 256x256 tiles run in whole-chip rounds (one workgroup per CU).  When the
-// tile count is just above a multiple of the CU count, the last round keeps
-// most CUs idle: the output columns of that partial round go to a second
-// launch with 128x128 tiles, which spreads them over the whole chip.
-template <class CBig, class CSmall>
-static int launch_big(LinearParams& p, hipStream_t s) {
-  const int cus = cu_count();
-  const int mt = (p.M + 255) / 256, nt = p.seg_n / 256;
-  const int64_t tiles = (int64_t)mt * nt;
-  const int64_t full = tiles / cus, rem = tiles - full * cus;
-  if (p.n_seg_count == 1 && full >= 1 && rem > 0 && rem * 4 < cus) {
-    const int n_main = (int)(full * cus / mt);
-    const int tail_cols = (nt - n_main) * 256;
-    const int64_t small = (int64_t)((p.M + 127) / 128) * (tail_cols / 128);
-    if (n_main >= 1 && tail_cols > 0 && small <= cus) {
-      LinearParams main = p;
-      main.seg_n = n_main * 256;
-      WAM_TRY(launch_gemm<CBig>(main, s));
-      LinearParams tail = p;
-      const int64_t c0 = (int64_t)n_main * 256;
-      tail.seg_n = tail_cols;
-      tail.n_off = p.n_off + (int)c0;
-      tail.w[0] = static_cast<const char*>(p.w[0]) + c0 * p.ldw * CBig::WB;
-      if (p.wscale[0]) tail.wscale[0] = p.wscale[0] + c0;
-      tail.bias[0] = p.bias[0] ? p.bias[0] + c0 : nullptr;
-      tail.out[0] = static_cast<char*>(p.out[0]) + c0 * (p.out_f32 ? 4 : 2);
-      if (p.res) tail.res = static_cast<const char*>(p.res) + c0 * (p.res_f32 ? 4 : 2);
-      return launch_gemm<CSmall>(tail, s);
-    }
+// tile count is not a multiple of the CU count, the last round keeps CUs idle.
+// The plan then runs the first `full` rounds' worth of whole output columns
+// as the main launch and the remaining columns (the tail) one of two ways:
+//   kind 1: 128x128 tiles over the whole chip; a round of them costs about
+//           0.375 of a 256x256 tile's time (measured at K = 3072 and 14336);
+//   kind 2: split-K: each 256x256 tail tile in ks k ranges (ks * tail tiles
+//           <= CUs), fp32 partial sums in the caller's workspace, then one
+//           reduce pass that applies the epilogue.  Cost per range 1/ks of a
+//           tile, plus about 4 k-tiles of pipeline fill, plus the reduce
+//           (a 256 KB partial per range at ~5 TB/s, against ~1.8 us per
+//           64-deep k-tile of a 256x256 tile).
+// Costs are in 256x256 tile times; the cheapest of one launch, kind 1 and
+// kind 2 (when the workspace holds its partials) wins.  E.g. 6240 x 3072 x
+// 14336: 250 tiles + 50 tail tiles in 5 ranges (1.25 vs 1.375 for kind 1).
+struct GemmPlan {
+  int kind;     // 0: one launch
+  int n_main;   // 256-column tiles of the main launch
+  int k_split;  // kind 2
+};
+
+static GemmPlan gemm_plan(int M, int seg_n, int n_seg, int K, int cus, int64_t ws_bytes) {
+  const GemmPlan one{0, 0, 1};
+  if (n_seg != 1 || seg_n % 256 != 0 || K % 64 != 0) return one;
+  const int mt = (M + 255) / 256, nt = seg_n / 256;
+  const int64_t tiles = (int64_t)mt * nt, full = tiles / cus;
+  if (full < 1 || tiles % cus == 0) return one;
+  const int n_main = (int)(full * cus / mt);
+  if (n_main < 1 || n_main >= nt) return one;
+  const int tail_cols = (nt - n_main) * 256;
+  const int64_t tail_tiles = (int64_t)mt * (nt - n_main);
+  const double nk = K / 64.0;
+  double best = (double)((tiles + cus - 1) / cus);
+  GemmPlan plan = one;
+  const int64_t small = (int64_t)((M + 127) / 128) * (tail_cols / 128);
+  const double cost1 = (double)full + (double)((small + cus - 1) / cus) * 0.375;
+  if (cost1 < best - 1e-9) best = cost1, plan = GemmPlan{1, n_main, 1};
+  const int64_t ks = cus / tail_tiles < 8 ? cus / tail_tiles : 8;
+  if (ks >= 2 && ks <= nk) {
+    const int64_t bytes = ks * M * (int64_t)tail_cols * 4;
+    const double cost2 = (double)full + 1.0 / ks + 4.0 / nk + (double)(tail_tiles * ks) * 0.052 / (nk * 1.8);
+    if (bytes <= ws_bytes && cost2 < best - 1e-9) best = cost2, plan = GemmPlan{2, n_main, (int)ks};
   }
-  return launch_gemm<CBig>(p, s);
+  return plan;
+}
+
+static int64_t plan_workspace(const GemmPlan& g, int M, int seg_n) {
+  return g.kind == 2 ? (int64_t)g.k_split * M * (int64_t)(seg_n - g.n_main * 256) * 4 : 0;
+}
+
+template <class CBig, class CSmall>
+static int launch_big(LinearParams& p, int64_t ws_bytes, hipStream_t s) {
+  const GemmPlan g = gemm_plan(p.M, p.seg_n, p.n_seg_count, p.K, cu_count(), p.part ? ws_bytes : 0);
+  if (g.kind == 0) return launch_gemm<CBig>(p, s);
+  LinearParams main = p;
+  main.seg_n = g.n_main * 256;
+  main.k_split = 1;
+  WAM_TRY(launch_gemm<CBig>(main, s));
+  LinearParams tail = p;
+  const int64_t c0 = (int64_t)g.n_main * 256;
+  tail.seg_n = p.seg_n - (int)c0;
+  tail.n_off = p.n_off + (int)c0;
+  tail.w[0] = static_cast<const char*>(p.w[0]) + c0 * p.ldw * CBig::WB;
+  if (p.wscale[0]) tail.wscale[0] = p.wscale[0] + c0;
+  tail.bias[0] = p.bias[0] ? p.bias[0] + c0 : nullptr;
+  tail.out[0] = static_cast<char*>(p.out[0]) + c0 * (p.out_f32 ? 4 : 2);
+  if (p.res) tail.res = static_cast<const char*>(p.res) + c0 * (p.res_f32 ? 4 : 2);
+  if (g.kind == 1) {
+    tail.k_split = 1;
+    return launch_gemm<CSmall>(tail, s);
+  }
+  tail.k_split = g.k_split;
+  return launch_gemm<CBig>(tail, s);
+}
+
+// Whether linear() takes the 256x256 path for this shape.
+static bool uses_big_tiles(int M, int seg_n, int n_seg) {
+  const int64_t big_tiles = (int64_t)((M + 255) / 256) * (seg_n / 256) * n_seg;
+  return seg_n % 256 == 0 && big_tiles >= 200;
+}
+
+int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K) {
+  if (M < 1 || seg_n < 1 || K < 1 || !uses_big_tiles(M, seg_n, n_seg)) return 0;
+  return plan_workspace(gemm_plan(M, seg_n, n_seg, K, cu_count(), INT64_MAX), M, seg_n);
 }
 
 int linear(const wam_linear_args* a, hipStream_t s) {
@@ -564,9 +699,13 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.n_seg_count = a->n_seg;
   p.mod_d = a->seg_n;
   p.n_off = 0;
-  const int64_t big_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 256) * a->n_seg;
+  WAM_REQUIRE(a->workspace_bytes >= 0, "wam_linear: negative workspace_bytes");
+  p.k_split = 1;
+  p.part = static_cast<float*>(a->workspace);
+  const int64_t ws_bytes = a->workspace ? a->workspace_bytes : 0;
+  const bool big = uses_big_tiles(a->M, a->seg_n, a->n_seg);
   if (f8) {
-    if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, s);
+    if (big) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, ws_bytes, s);
     return launch_gemm<Cfg128x128f8>(p, s);
   }
   const char* force = getenv("WAM_GEMM_CFG");
@@ -577,7 +716,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return rc;
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  if (a->seg_n % 256 == 0 && big_tiles >= 200) return launch_big<Cfg256x256w8t, Cfg128x128w4>(p, s);
+  if (big) return launch_big<Cfg256x256w8t, Cfg128x128w4>(p, ws_bytes, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);
@@ -635,4 +774,8 @@ extern "C" int wam_quantize_fp8_rows(const void* w, int rows, int cols, int64_t 
 
 extern "C" int wam_linear(const wam_linear_args* args, void* stream) {
   return wam::linear(args, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t wam_linear_workspace_bytes(int M, int N, int n_seg, int K) {
+  return wam::linear_workspace_bytes(M, N, n_seg, K);
 }

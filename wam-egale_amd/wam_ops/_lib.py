@@ -40,7 +40,8 @@ class LinearArgs(Structure):
                 ("epilogue", c_int), ("res", c_void_p), ("ldr", c_int64),
                 ("res_dtype", c_int), ("out_dtype", c_int),
                 ("gate", Modulation), ("gate_index", c_int),
-                ("w_dtype", c_int), ("w_scale", c_void_p * 3)]
+                ("w_dtype", c_int), ("w_scale", c_void_p * 3),
+                ("workspace", c_void_p), ("workspace_bytes", c_int64)]
 
 
 class LnArgs(Structure):
@@ -136,6 +137,7 @@ STRUCTS = {
 SIGNATURES = {
     "wam_linear": (c_int, [POINTER(LinearArgs), c_void_p]),
     "wam_attention_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
+    "wam_linear_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "wam_quantize_fp8_rows": (c_int, [c_void_p, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
     "wam_ln_modulate": (c_int, [POINTER(LnArgs), c_void_p]),
     "wam_rms_rope": (c_int, [POINTER(RmsRopeArgs), c_void_p]),

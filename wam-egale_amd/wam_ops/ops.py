@@ -170,7 +170,15 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         _req(table is not None and temb is not None and gate_index is not None, "gate needs table/temb")
         a.gate = modulation(table, temb, tokens if tokens is not None else M)
         a.gate_index = gate_index
+    scratch = None
+    nbytes = _lib.lib().wam_linear_workspace_bytes(M, N, len(ws), K)
+    if nbytes > 0:
+        # fp32 partial sums of the split-K tail
+        scratch = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = scratch.data_ptr(), nbytes
     _lib.check(_lib.lib().wam_linear(ctypes.byref(a), stream_handle(dev)), "wam_linear")
+    if scratch is not None:
+        scratch.record_stream(torch.cuda.current_stream(dev))
     return outs[0] if single else outs
 
 
