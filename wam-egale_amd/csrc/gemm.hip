@@ -167,10 +167,12 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
 
 // The epilogue of 4 consecutive outputs (m, n..n+3) from their fp32 sums v:
 // fp8 column scale, bias, then GELU-tanh, or the (gated) residual with an
-// fp32 or bf16 output.
+// fp32 or bf16 output.  gate_pre: the gate of these columns when the caller
+// already holds it (every row it handles reads the same modulation row).
 template <int EPI, int WB>
 __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int m, int n, const f32x4 v,
-                                          const float (&bv)[4], const float (&wsc)[4]) {
+                                          const float (&bv)[4], const float (&wsc)[4],
+                                          const float* gate_pre = nullptr) {
   float y[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
@@ -190,7 +192,12 @@ __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int 
     }
     if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
       float gt[4];
-      ld_mod4(p.gate, p.mod_d, m, p.gate_index, n + p.n_off, gt);
+      if (gate_pre) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gt[e] = gate_pre[e];
+      } else {
+        ld_mod4(p.gate, p.mod_d, m, p.gate_index, n + p.n_off, gt);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
     } else {
@@ -407,6 +414,14 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     const float4 t = n_ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
+  // The gate of this lane's 4 columns, once per tile when all the tile's rows
+  // read the same modulation row (one sample, or one latent frame).
+  float gate[4] = {0.f, 0.f, 0.f, 0.f};
+  bool gate_once = false;
+  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + C::BM, p.M) - 1);
+    if (gate_once && n_ok) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
+  }
   __syncthreads();  // every wave is done reading the last stage
 #pragma unroll
   for (int rd = 0; rd < NROUNDS; ++rd) {
@@ -439,7 +454,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       if constexpr (EPI == kEpiPartial) {
         *reinterpret_cast<f32x4*>(p.part + ((int64_t)kp * p.M + m) * p.seg_n + n) = v;
       } else {
-        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc);
+        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate_once ? gate : nullptr);
       }
     }
     if (rd + 1 < NROUNDS) __syncthreads();
