@@ -134,18 +134,19 @@ __device__ inline i32x4 make_rsrc4(const void* p, uint32_t bytes) {
 // load with explicit s_waitcnt vmcnt and barriers.  Lane L writes bytes
 // [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
 __device__ inline void asm_ld16_lds(i32x4 rsrc, void* lds, int voff) {
-  // The low 32 bits of a generic pointer into LDS are the LDS byte offset.
+  // The low 32 bits of a generic pointer into LDS are the LDS byte offset;
+  // it goes to M0 as an operand of the statement, so the compiler writes M0
+  // itself and knows its value.  One wait state between that write and the
+  // LDS DMA that reads it.
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  // One wait state between the M0 write and the LDS DMA that reads it.
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voff), "s"(rsrc), "s"(m0) : "memory", "m0");
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voff), "s"(rsrc), "{m0}"(m0) : "memory");
 }
 
 // Same for a per-lane 64-bit global address (global_load_lds_dwordx4).
 __device__ inline void asm_g_ld16_lds(uint64_t gaddr, void* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(gaddr), "s"(m0) : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gaddr), "{m0}"(m0) : "memory");
 }
 
 // 16 bytes per lane from a buffer resource straight into LDS: lane L writes
