@@ -44,6 +44,9 @@ def _inputs(shape, B, grid, Lc, seed, per_token=False):
     (TINY, 1, (3, 4, 5), 16, False),
     (TINY, 2, (2, 5, 7), 24, True),
     (dict(dim=3072, heads=24, ffn=14336), 1, (4, 8, 8), 512, False),
+    # the Wan-1.3B-shaped block of the CPU reference case: 1024 tokens on a
+    # (4, 16, 16) grid, dim 1536, 12 heads, FFN 8960, 512 context tokens
+    (dict(dim=1536, heads=12, ffn=8960), 1, (4, 16, 16), 512, False),
 ])
 def test_block_vs_fp32_oracle(dev, cfg, B, grid, Lc, per_token):
     from wam_ops import synthetic
