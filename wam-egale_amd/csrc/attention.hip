@@ -85,7 +85,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   split = __builtin_amdgcn_readfirstlane(split);
   ns = __builtin_amdgcn_readfirstlane(ns);
   const int qt = unit % nqt, bh = unit / nqt;
-  const int h = bh % a.H, b = bh / a.H;
+  const int b = bh % a.B, h = bh / a.B;  // head-major: the batch rows of one head are adjacent
 
   const int n_hist = a.n_hist_dev ? __builtin_amdgcn_readfirstlane(*a.n_hist_dev) : 0;
   const int n_tot = n_hist + a.Mk;
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
   const int qt = unit % nqt, bh = unit / nqt;
   const int qi = qt * QT + qq;
   if (qi >= a.Mq) return;
-  const int h = bh % a.H, b = bh / a.H;
+  const int b = bh % a.B, h = bh / a.B;  // head-major: the batch rows of one head are adjacent
   const float* ml = part + (int64_t)n_split * rows * kAttnHD;
   float2 mlv[kAttnMaxSplit], ov[kAttnMaxSplit];
 #pragma unroll
