@@ -731,7 +731,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return rc;
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  if (big) return launch_big<Cfg256x256w8t, Cfg128x128w4>(p, ws_bytes, s);
+  if (big) return launch_big<Cfg256x256w8s, Cfg128x128w4>(p, ws_bytes, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);
