@@ -371,9 +371,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
 
 // Launch plan of the split path: the first n_full units run whole, the other
 // n_tail units are split into n_split key ranges each.  Cost model, in units
-// of one whole unit's run time on one CU (kt key tiles of 64 keys), for 256
-// CUs taking workgroups in dispatch order:
-//   n_full / 256  +  ceil(pieces / 256) * (1 / n_split + kFill / kt)
+// of one whole unit's run time on one CU (kt key tiles of 64 keys), for C
+// CUs (256 on MI355X) taking workgroups in dispatch order:
+//   n_full / C  +  ceil(pieces / C) * (1 / n_split + kFill / kt)
 //                 +  pieces * kCombine / kt,         pieces = n_tail * n_split
 // kFill: key tiles' worth of pipeline fill and partial-result store per
 // piece; kCombine: the combine's time per piece (a 133 KB fp32 partial at
@@ -384,7 +384,6 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
 struct AttnPlan {
   int n_full, n_split, n_tail;
 };
-constexpr int kPlanCUs = 256;
 constexpr int64_t kPartBytesPerPiece = (int64_t)kAttnSplitQT * (kAttnHD + 2) * 4;
 
 static int64_t plan_bytes(const AttnPlan& p) {
@@ -392,19 +391,20 @@ static int64_t plan_bytes(const AttnPlan& p) {
 }
 
 static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_bytes) {
+  const int cus = device_cu_count();
   constexpr double kFill = 1.5, kCombine = 0.0133;
   const int64_t units = (int64_t)((Mq + kAttnSplitQT - 1) / kAttnSplitQT) * H * B;
   AttnPlan best{(int)units, 1, 0};
   if (units <= 0 || units >= (1 << 26)) return best;
   const double kt = (double)((keys > 0 ? keys : 1) + kAttnKT - 1) / kAttnKT;
-  double best_cost = (double)((units + kPlanCUs - 1) / kPlanCUs);
-  for (int64_t F = 0; F < units; F += kPlanCUs) {
+  double best_cost = (double)((units + cus - 1) / cus);
+  for (int64_t F = 0; F < units; F += cus) {
     const int64_t T = units - F;
     for (int ns = 2; ns <= kAttnMaxSplit; ++ns) {
       const int64_t pieces = T * ns;
       if (pieces * kPartBytesPerPiece > max_bytes) break;
-      const double cost = (double)F / kPlanCUs +
-                          (double)((pieces + kPlanCUs - 1) / kPlanCUs) * (1.0 / ns + kFill / kt) +
+      const double cost = (double)F / cus +
+                          (double)((pieces + cus - 1) / cus) * (1.0 / ns + kFill / kt) +
                           (double)pieces * kCombine / kt;
       if (cost < best_cost - 1e-9) {
         best_cost = cost;

@@ -566,18 +566,6 @@ static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool
   return WAM_OK;
 }
 
-static int cu_count() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // 256x256 tiles run in whole-chip rounds (one workgroup per CU).  When the
 // tile count is not a multiple of the CU count, the last round keeps CUs idle.
 // The plan then runs the first `full` rounds' worth of whole output columns
@@ -630,7 +618,7 @@ static int64_t plan_workspace(const GemmPlan& g, int M, int seg_n) {
 
 template <class CBig, class CSmall>
 static int launch_big(LinearParams& p, int64_t ws_bytes, hipStream_t s) {
-  const GemmPlan g = gemm_plan(p.M, p.seg_n, p.n_seg_count, p.K, cu_count(), p.part ? ws_bytes : 0);
+  const GemmPlan g = gemm_plan(p.M, p.seg_n, p.n_seg_count, p.K, device_cu_count(), p.part ? ws_bytes : 0);
   if (g.kind == 0) return launch_gemm<CBig>(p, s);
   LinearParams main = p;
   main.seg_n = g.n_main * 256;
@@ -661,7 +649,7 @@ static bool uses_big_tiles(int M, int seg_n, int n_seg) {
 
 int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K) {
   if (M < 1 || seg_n < 1 || K < 1 || !uses_big_tiles(M, seg_n, n_seg)) return 0;
-  return plan_workspace(gemm_plan(M, seg_n, n_seg, K, cu_count(), INT64_MAX), M, seg_n);
+  return plan_workspace(gemm_plan(M, seg_n, n_seg, K, device_cu_count(), INT64_MAX), M, seg_n);
 }
 
 int linear(const wam_linear_args* a, hipStream_t s) {

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdarg.h>
+#include <atomic>
 #include "../../include/wam_block.h"
 
 namespace wam {
@@ -71,6 +72,21 @@ __host__ __device__ inline int xcd_remap(int i, int n) {
   const int q = n >> 3, r = n & 7;
   const int x = i & 7, k = i >> 3;
   return x * q + (x < r ? x : r) + k;
+}
+
+// Compute units of the current device (cached per device; 256 when the
+// query fails, e.g. without a GPU).  Launch plans size their dispatch rounds
+// with it.
+inline int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 // --------------------------------------------------------------- device side
