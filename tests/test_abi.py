@@ -107,6 +107,7 @@ def test_linear_split_k_plan_workspace():
     # 6240 x 3072 -> 14336 (FFN1): 1275 whole tiles, 125 tail tiles in 2 ranges
     assert h.wam_linear_workspace_bytes(6240, 14336, 1, 3072) == 2 * 6240 * 1280 * 4
     assert h.wam_linear_workspace_bytes(6240, 2816, 1, 3072) == 8 * 6240 * 256 * 4
+    assert h.wam_linear_workspace_bytes(3900, 4352, 1, 4160) == 8 * 3900 * 256 * 4
     # short k (3072 -> 3072) keeps the 128x128 tail; 4680 rows leave no
     # partial round worth splitting; QKV (three segments) is never split
     assert h.wam_linear_workspace_bytes(6240, 3072, 1, 3072) == 0
