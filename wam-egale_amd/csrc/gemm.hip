@@ -167,12 +167,13 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
 
 // The epilogue of 4 consecutive outputs (m, n..n+3) from their fp32 sums v:
 // fp8 column scale, bias, then GELU-tanh, or the (gated) residual with an
-// fp32 or bf16 output.  gate_pre: the gate of these columns when the caller
-// already holds it (every row it handles reads the same modulation row).
+// fp32 or bf16 output.  With gate_held the gate of these columns is
+// gate_pre (every row the caller handles reads the same modulation row);
+// otherwise it is read for row m.
 template <int EPI, int WB>
 __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int m, int n, const f32x4 v,
                                           const float (&bv)[4], const float (&wsc)[4],
-                                          const float* gate_pre = nullptr) {
+                                          const float (&gate_pre)[4], bool gate_held) {
   float y[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
@@ -192,7 +193,7 @@ __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int 
     }
     if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
       float gt[4];
-      if (gate_pre) {
+      if (gate_held) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) gt[e] = gate_pre[e];
       } else {
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       if constexpr (EPI == kEpiPartial) {
         *reinterpret_cast<f32x4*>(p.part + ((int64_t)kp * p.M + m) * p.seg_n + n) = v;
       } else {
-        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate_once ? gate : nullptr);
+        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate, gate_once);
       }
     }
     if (rd + 1 < NROUNDS) __syncthreads();
@@ -497,7 +498,8 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p)
     const float4 t = *reinterpret_cast<const float4*>(p.wscale[0] + n);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
-  epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc);
+  const float no_gate[4] = {0.f, 0.f, 0.f, 0.f};
+  epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false);
 }
 
 template <class C>
