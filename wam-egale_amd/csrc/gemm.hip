@@ -443,7 +443,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
         }
     }
     __syncthreads();
-#pragma unroll
+#pragma unroll 4
     for (int it = 0; it < ROUND / (C::kWaves * RPI); ++it) {
       const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
       const int row = rd * ROUND + rr;
