@@ -47,7 +47,8 @@ struct GemmCfg {
   static constexpr int WB = WB_;          // bytes per weight element: 2 (bf16) or 1 (fp8 e4m3)
   // SPLIT > 1: a stage's loads are issued in SPLIT parts, one at the barrier
   // and the others before the MFMAs of the next k-step's first sub-steps, so
-  // the load issue does not stall the waves all at once (needs STAGES >= 3).
+  // the load issue does not stall the waves all at once.  With two stages
+  // the later parts have most of a k-step to land before the next barrier.
   static constexpr int SPLIT = SPLIT_;
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
   static constexpr int SCHED = SCHED_;    // 1: alternate DS reads and MFMAs; 2: all reads of
@@ -73,7 +74,7 @@ struct GemmCfg {
                 "loads per wave: A then W");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(STAGES >= 2 && BLOCKS * (STAGES * STAGE + (5 - STAGES) * 1024) <= 160 * 1024, "LDS budget");
-  static_assert(SPLIT == 1 || (STAGES >= 3 && LOADS_PER_WAVE % SPLIT == 0 && SPLIT - 1 <= BK / 16 - 1),
+  static_assert(SPLIT == 1 || (STAGES >= 2 && LOADS_PER_WAVE % SPLIT == 0 && SPLIT - 1 <= BK / 16 - 1),
                 "split load issue");
 };
 
@@ -469,6 +470,7 @@ using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
 using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
 using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
 using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
+using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
 using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
 using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
 // fp8 e4m3 weights (64-byte LDS weight rows, three stages, loads issued in
@@ -561,6 +563,7 @@ static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool
   if (!strcmp(name, "128x128w4")) return launch_gemm<Cfg128x128w4>(p, s);
   if (!strcmp(name, "256x256w8s")) return launch_gemm<Cfg256x256w8s>(p, s);
   if (!strcmp(name, "256x256w8t")) return launch_gemm<Cfg256x256w8t>(p, s);
+  if (!strcmp(name, "256x256w8t2")) return launch_gemm<Cfg256x256w8t2>(p, s);
   if (!strcmp(name, "256x256k32w8t4")) return launch_gemm<Cfg256x256k32w8t4>(p, s);
   if (!strcmp(name, "256x128k32w4b2s")) return launch_gemm<Cfg256x128k32w4b2s>(p, s);
   if (!strcmp(name, "256x256k32w8t4s2")) return launch_gemm<Cfg256x256k32w8t4s2>(p, s);
@@ -721,7 +724,7 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return rc;
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  if (big) return launch_big<Cfg256x256w8s, Cfg128x128w4>(p, ws_bytes, s);
+  if (big) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);
