@@ -473,9 +473,9 @@ using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
 using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
 using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
 using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
-// fp8 e4m3 weights (64-byte LDS weight rows, three stages, loads issued in
-// three parts)
-using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 3, 1, 2, 1, 3>;
+// fp8 e4m3 weights (64-byte LDS weight rows, two stages, loads issued in
+// two parts)
+using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 1, 2>;
 using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
 using Cfg256x256k32w8t4s2 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2, 2, 2>;
 
