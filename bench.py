@@ -374,7 +374,8 @@ def main():
         def vstep():
             with torch.no_grad():
                 return vlayer(xv, ctxv, tembv, freqv, candidate_cache_rows=rows)
-        # candidate_cache_rows are validated on the host per call, as the reference does
+        # candidate_cache_rows are read back and validated on the host the first time this
+        # tensor is seen (again after any in-place write), as the reference checks them
         vms = timed_steps(vstep, args.steps, args.warmup)
         g, a = layer_flops(Mv, D, F, Lc, self_keys=prefix + Mv, batch=B)
         out["lverify"] = {"tokens": B * Mv, "us_per_layer": round(vms * 1e3, 1),

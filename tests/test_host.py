@@ -152,3 +152,25 @@ def test_block_stack_contract_on_host():
             stack(x, x, None, None, candidate_cache_rows=rows)
     with pytest.raises(ValueError):
         BlockStack([])
+
+
+def test_candidate_rows_validation_reuse():
+    """The rows check (model.py:639-647) reads the rows back once per tensor;
+    the same unmodified tensor passes again without a read, and any in-place
+    write, another tensor, or another pool size is checked afresh."""
+    from wam_ops.native import validate_candidate_rows
+    dev = torch.device("cpu")
+    rows = torch.tensor([0, 1, 1, 0], dtype=torch.long)
+    validate_candidate_rows(rows, 4, 2, dev)
+    validate_candidate_rows(rows, 4, 2, dev)          # cached
+    rows[2] = 2                                       # in-place write: out of range now
+    with pytest.raises(ValueError, match="candidate_cache_rows"):
+        validate_candidate_rows(rows, 4, 2, dev)
+    validate_candidate_rows(rows, 4, 3, dev)          # a larger pool admits it
+    with pytest.raises(ValueError, match="candidate_cache_rows"):
+        validate_candidate_rows(rows, 4, 2, dev)      # the cache is keyed by pool size
+    bad = torch.tensor([0, -1, 0, 0], dtype=torch.long)
+    with pytest.raises(ValueError, match="candidate_cache_rows"):
+        validate_candidate_rows(bad, 4, 2, dev)
+    with pytest.raises(ValueError, match="candidate_cache_rows"):
+        validate_candidate_rows(rows, 3, 3, dev)      # wrong batch
