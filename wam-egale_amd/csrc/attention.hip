@@ -116,7 +116,26 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   // lands in row 4 (g % 16) + L / 16, physical chunk L % 16, and fetches the
   // logical chunk the swizzle maps there.  Load i of wave w is g = w + i W.
   const int lrow = lane >> 4, pch = lane & 15;
-  auto issue = [=](int t, char* base) {
+  // The wave's loads cover 16 / W blocks of 4 keys (K and V of a block share
+  // their rows).  Their pool slots are read with wave-uniform loads before
+  // the wait and barrier that precede the issue, so that the loads' latency
+  // overlaps that wait.
+  constexpr int NB = 16 / W;
+  struct TileSlots { int v[NB][4]; };
+  auto tile_slots = [=](int t) {
+    TileSlots ts;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int jj = t * kAttnKT + 4 * ((wave + b * W) & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = __builtin_amdgcn_readfirstlane(min(jj + r, n_tot - 1));
+        ts.v[b][r] = j < n_hist ? slots[j] : 0;
+      }
+    }
+    return ts;
+  };
+  auto issue = [=](int t, char* base, TileSlots ts) {
     const int j0 = t * kAttnKT;
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
@@ -124,15 +143,9 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
       const bool is_k = i < 16 / W;                 // compile-time per i
       const int gb = g & 15;
       const int row = 4 * gb + lrow;
-      // slot indices of the block's 4 rows: wave-uniform loads
       const int jj = j0 + 4 * gb;
-      int sl[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = __builtin_amdgcn_readfirstlane(min(jj + r, n_tot - 1));
-        sl[r] = j < n_hist ? slots[j] : 0;
-      }
-      const int slot = lrow == 0 ? sl[0] : (lrow == 1 ? sl[1] : (lrow == 2 ? sl[2] : sl[3]));
+      const int b = i % NB;                         // block (wave + b W) & 15 == gb
+      const int slot = lrow == 0 ? ts.v[b][0] : (lrow == 1 ? ts.v[b][1] : (lrow == 2 ? ts.v[b][2] : ts.v[b][3]));
       const int j = min(jj + lrow, n_tot - 1);
       const int c = is_k ? (pch ^ (row & 15)) : (pch ^ ((row & 3) << 2));
       const bf16* src = j < n_hist ? (is_k ? pool_k : pool_v) + (int64_t)slot * a.pool_rstride
@@ -159,7 +172,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   const int ntiles = (int)((int64_t)(split + 1) * all_tiles / ns) - t_first;
 #pragma unroll
   for (int st = 0; st < kAttnStages - 1; ++st)
-    if (st < ntiles) issue(t_first + st, WAM_ATTN_BUF(st));
+    if (st < ntiles) issue(t_first + st, WAM_ATTN_BUF(st), tile_slots(t_first + st));
 
   // The tile loop is unrolled by the stage count so that every LDS reference
   // is to a fixed __shared__ object.
@@ -168,6 +181,9 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
     for (int st = 0; st < kAttnStages; ++st) {
       const int t = t0 + st;
       if (t >= ntiles) break;
+      const bool refill = t + kAttnStages - 1 < ntiles;
+      TileSlots ts{};
+      if (refill) ts = tile_slots(t_first + t + kAttnStages - 1);
       if (t + kAttnStages - 2 < ntiles) {
         // stages t+1 .. t+STAGES-2 may still be in flight
         __builtin_amdgcn_s_waitcnt((((kAttnStages - 2) * LPW) & 15) | ((((kAttnStages - 2) * LPW) >> 4) << 14) |
@@ -176,8 +192,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
       }
       __builtin_amdgcn_s_barrier();
-      if (t + kAttnStages - 1 < ntiles)
-        issue(t_first + t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages));
+      if (refill) issue(t_first + t + kAttnStages - 1, WAM_ATTN_BUF((st + kAttnStages - 1) % kAttnStages), ts);
       if (!live) continue;  // this wave's queries are all past Mq; it still loads and syncs
       const char* kb = WAM_ATTN_BUF(st);
       const char* vb = kb + kAttnTile;
