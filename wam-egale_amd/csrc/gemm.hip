@@ -168,13 +168,14 @@ __device__ __forceinline__ void fetch_frags(const char* abase, const char* bbase
 
 // The epilogue of 4 consecutive outputs (m, n..n+3) from their fp32 sums v:
 // fp8 column scale, bias, then GELU-tanh, or the (gated) residual with an
-// fp32 or bf16 output.  With gate_held the gate of these columns is
+// fp32 or bf16 output.  The caller loads the residual rv (fp32) of the
+// residual epilogues.  With gate_held the gate of these columns is
 // gate_pre (every row the caller handles reads the same modulation row);
 // otherwise it is read for row m.
 template <int EPI, int WB>
 __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int m, int n, const f32x4 v,
                                           const float (&bv)[4], const float (&wsc)[4],
-                                          const float (&gate_pre)[4], bool gate_held) {
+                                          const float (&gate_pre)[4], bool gate_held, const float (&rv)[4]) {
   float y[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? v[e] * wsc[e] + bv[e] : v[e] + bv[e];
@@ -182,16 +183,6 @@ __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int 
 #pragma unroll
     for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
   } else if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
-    float rv[4];
-    const int64_t ro = (int64_t)m * p.ldr + n;
-    if (p.res_f32) {
-      const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
-      rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
-    } else {
-      const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
-    }
     if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
       float gt[4];
       if (gate_held) {
@@ -424,7 +415,37 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + C::BM, p.M) - 1);
     if (gate_once && n_ok) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
   }
-  __syncthreads();  // every wave is done reading the last stage
+  // The residual of a round's rows is loaded into registers before the round
+  // is staged through LDS (16 bytes per row chunk: 4 fp32, or 4 bf16 in the
+  // low half), so the whole round's loads are in flight together.
+  constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
+  constexpr int ITERS = ROUND / (C::kWaves * RPI);
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  u32x4v rraw[RES ? ITERS : 1];
+  auto res_prefetch = [&](int rd) {
+    if constexpr (RES) {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;
+        const int row = rd * ROUND + rr;
+        const int m = m0 + row;
+        if (row >= C::BM || m >= p.M || !n_ok) continue;
+        const int64_t ro = (int64_t)m * p.ldr + n;
+        if (p.res_f32) {
+          rraw[it] = *reinterpret_cast<const u32x4v*>(static_cast<const float*>(p.res) + ro);
+        } else {
+          const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const bf16*>(p.res) + ro);
+          rraw[it] = u32x4v{t[0], t[1], 0u, 0u};
+        }
+      }
+    }
+  };
+  res_prefetch(0);
+  // Every wave is done reading the last stage (its fragments are in
+  // registers and consumed); only LDS operations are waited for, so the
+  // residual loads stay in flight.
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int rd = 0; rd < NROUNDS; ++rd) {
 #pragma unroll
@@ -443,9 +464,10 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
           *reinterpret_cast<f32x4*>(buf + lr * ROW_B + ((qq ^ (lr & 15)) << 4)) = v;
         }
     }
-    __syncthreads();
-#pragma unroll 4
-    for (int it = 0; it < ROUND / (C::kWaves * RPI); ++it) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are done
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
       const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
       const int row = rd * ROUND + rr;
       const int m = m0 + row;
@@ -456,10 +478,27 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       if constexpr (EPI == kEpiPartial) {
         *reinterpret_cast<f32x4*>(p.part + ((int64_t)kp * p.M + m) * p.seg_n + n) = v;
       } else {
-        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate, gate_once);
+        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (RES) {
+          const u32x4v t = rraw[it];
+          if (p.res_f32) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rv[e] = __uint_as_float(t[e]);  // by value: a vector element has no address
+          } else {
+            rv[0] = __uint_as_float(t[0] << 16);
+            rv[1] = __uint_as_float(t[0] & 0xffff0000u);
+            rv[2] = __uint_as_float(t[1] << 16);
+            rv[3] = __uint_as_float(t[1] & 0xffff0000u);
+          }
+        }
+        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate, gate_once, rv);
       }
     }
-    if (rd + 1 < NROUNDS) __syncthreads();
+    if (rd + 1 < NROUNDS) {
+      res_prefetch(rd + 1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // this round's LDS reads are done
+      __builtin_amdgcn_s_barrier();
+    }
   }
 #undef WAM_GEMM_BUF
 }
@@ -501,7 +540,19 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p)
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
   const float no_gate[4] = {0.f, 0.f, 0.f, 0.f};
-  epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false);
+  float rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
+    const int64_t ro = (int64_t)m * p.ldr + n;
+    if (p.res_f32) {
+      const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
+      rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
+    } else {
+      const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
+    }
+  }
+  epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false, rv);
 }
 
 template <class C>
