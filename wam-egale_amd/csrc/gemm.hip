@@ -289,6 +289,41 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     b_lane = wrow * b_pitch + wch * 16;
   }
 
+  // The epilogue's per-column operands are loaded before the k loop, so that
+  // their latency is not at the end of the tile.
+  constexpr int RPO = (C::STAGE / (C::BN * 4)) / 32 * 32;  // fp32 rows per buffer
+  static_assert(RPO >= 32, "a stage buffer must hold 32 fp32 rows of the tile");
+  constexpr int ROUND = RPO * C::STAGES;                 // rows staged per round
+  constexpr int NROUNDS = (C::BM + ROUND - 1) / ROUND;
+  constexpr int QPR = C::BN / 4;                         // 16-byte chunks per fp32 row
+  constexpr int RPI = 64 / QPR;                          // rows per wave-wide access
+  static_assert(QPR == 64 || QPR == 32, "BN must be 256 or 128");
+  constexpr int ROW_B = C::BN * 4;
+  void* out = seg == 0 ? p.out[0] : (seg == 1 ? p.out[1] : p.out[2]);
+  const bf16* __restrict__ bias = seg == 0 ? p.bias[0] : (seg == 1 ? p.bias[1] : p.bias[2]);
+  const int q = lane % QPR;  // this lane's chunk of a row in the read phase
+  const int n = n0 + 4 * q;
+  const bool n_ok = n < p.seg_n;  // N is a multiple of 4: a lane's 4 columns are all in or all out
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (bias && n_ok) {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
+  }
+  float wsc[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (C::WB == 1) {
+    const float* ws = seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2]);
+    const float4 t = n_ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
+    wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
+  }
+  // The gate of this lane's 4 columns, once per tile when all the tile's rows
+  // read the same modulation row (one sample, or one latent frame).
+  float gate[4] = {0.f, 0.f, 0.f, 0.f};
+  bool gate_once = false;
+  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + C::BM, p.M) - 1);
+    if (gate_once && n_ok) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
+  }
   f32x16 acc[C::TN][C::TM];
 #pragma unroll
   for (int j = 0; j < C::TN; ++j)
@@ -382,39 +417,6 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // residual and output accesses are contiguous and fill whole cache lines.
   // Rows are 16-byte chunks XOR-swizzled by (row & 15), which keeps both the
   // column-wise writes and the row-wise reads free of bank conflicts.
-  constexpr int RPO = (C::STAGE / (C::BN * 4)) / 32 * 32;  // fp32 rows per buffer
-  static_assert(RPO >= 32, "a stage buffer must hold 32 fp32 rows of the tile");
-  constexpr int ROUND = RPO * C::STAGES;                 // rows staged per round
-  constexpr int NROUNDS = (C::BM + ROUND - 1) / ROUND;
-  constexpr int QPR = C::BN / 4;                         // 16-byte chunks per fp32 row
-  constexpr int RPI = 64 / QPR;                          // rows per wave-wide access
-  static_assert(QPR == 64 || QPR == 32, "BN must be 256 or 128");
-  constexpr int ROW_B = C::BN * 4;
-  void* out = seg == 0 ? p.out[0] : (seg == 1 ? p.out[1] : p.out[2]);
-  const bf16* __restrict__ bias = seg == 0 ? p.bias[0] : (seg == 1 ? p.bias[1] : p.bias[2]);
-  const int q = lane % QPR;  // this lane's chunk of a row in the read phase
-  const int n = n0 + 4 * q;
-  const bool n_ok = n < p.seg_n;  // N is a multiple of 4: a lane's 4 columns are all in or all out
-  float bv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (bias && n_ok) {
-    const bf16x4 t = *reinterpret_cast<const bf16x4*>(bias + n);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
-  }
-  float wsc[4] = {1.f, 1.f, 1.f, 1.f};
-  if constexpr (C::WB == 1) {
-    const float* ws = seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2]);
-    const float4 t = n_ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
-    wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
-  }
-  // The gate of this lane's 4 columns, once per tile when all the tile's rows
-  // read the same modulation row (one sample, or one latent frame).
-  float gate[4] = {0.f, 0.f, 0.f, 0.f};
-  bool gate_once = false;
-  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + C::BM, p.M) - 1);
-    if (gate_once && n_ok) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
-  }
   // The residual of a round's rows is loaded into registers before the round
   // is staged through LDS (16 bytes per row chunk: 4 fp32, or 4 bf16 in the
   // low half), so the whole round's loads are in flight together.
