@@ -54,10 +54,12 @@ def test_linear_bias(dev, M, K, N, nseg):
 # modulation table).  (6240, 3072, 2816) and (6240, 6144, 3072) run their last
 # columns split over k (8 and 5 ranges of fp32 partials, then a reduce pass
 # with the epilogue); (3900, 4160, 4352) does so with a partial last row tile
-# and 65 k-tiles in 8 uneven ranges.
+# and 65 k-tiles in 8 uneven ranges.  (300, 512, 200) ends in a partial
+# column tile (72 of 128 columns), so lanes past N skip the residual loads
+# issued ahead of the LDS staging as well as the stores.
 @pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
                                    (4680, 256, 14336), (6240, 3072, 2816), (6240, 6144, 3072),
-                                   (3900, 4160, 4352)])
+                                   (3900, 4160, 4352), (300, 512, 200)])
 def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     D = N
