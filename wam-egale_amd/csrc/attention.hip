@@ -60,6 +60,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   __shared__ __attribute__((aligned(1024))) char lds0[kAttnStage];
   __shared__ __attribute__((aligned(1024))) char lds1[kAttnStage];
   __shared__ __attribute__((aligned(1024))) char lds2[kAttnStage];
+  // Each wave's 32 query rows (8 KB), laid out like a K tile.
+  __shared__ __attribute__((aligned(1024))) char ldsq[32 * W * kAttnHD * 2];
   static_assert(kAttnStages == 3, "three stage objects");
 #define WAM_ATTN_BUF(st) ((st) == 0 ? lds0 : (st) == 1 ? lds1 : lds2)
   const int tid = threadIdx.x, lane = tid & 63;
@@ -102,14 +104,6 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   const int qi = qt * QT + wave * 32 + l32;
   const bool q_ok = qi < a.Mq;
   const bool live = qt * QT + wave * 32 < a.Mq;  // wave-uniform
-  const bf16* qp = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride +
-                   (int64_t)(q_ok ? qi : 0) * a.q_rstride + h * kAttnHD + half * 8;
-  bf16x8 qf[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) {
-    qf[ks] = ld_bf16x8(qp + ks * 16);
-    if (!q_ok) qf[ks] = bf16x8{};
-  }
 
   // Direct-to-LDS staging.  Load g (0..31) of a stage fills 1 KB block g:
   // blocks 0-15 are the K tile, 16-31 the V tile, 4 rows (keys) each; lane L
@@ -170,9 +164,40 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   const int all_tiles = (n_tot + kAttnKT - 1) / kAttnKT;
   const int t_first = (int)((int64_t)split * all_tiles / ns);
   const int ntiles = (int)((int64_t)(split + 1) * all_tiles / ns) - t_first;
+  // Q comes in through LDS too, ahead of the first stages: loads of the
+  // wave's 32 rows, 4 rows (1 KB) per load, lane L fetching the logical chunk
+  // that the K-tile swizzle puts at byte 16 L.  The stage waits below count
+  // these loads, and the fragments are then read with ds_read, so no wait
+  // for Q also waits for the stages behind it.
+  char* const qbuf = ldsq + wave * (32 * kAttnHD * 2);
+  {
+    const bf16* qrow0 = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride + h * kAttnHD;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 4 * i + lrow;
+      const int qr = min(qt * QT + wave * 32 + row, a.Mq - 1);
+      const int c = pch ^ (row & 15);
+      asm_g_ld16_lds((uint64_t)(uintptr_t)(qrow0 + (int64_t)qr * a.q_rstride + c * 8), qbuf + i * 1024);
+    }
+  }
 #pragma unroll
   for (int st = 0; st < kAttnStages - 1; ++st)
     if (st < ntiles) issue(t_first + st, WAM_ATTN_BUF(st), tile_slots(t_first + st));
+  // This wave's Q loads are done once at most the stage loads behind them
+  // are outstanding.
+  static_assert(kAttnStages == 3 && 2 * LPW < 64, "Q wait: vmcnt range");
+  constexpr int kVm1 = (LPW & 15) | ((LPW >> 4) << 14) | (7 << 4) | (15 << 8);
+  constexpr int kVm2 = ((2 * LPW) & 15) | (((2 * LPW) >> 4) << 14) | (7 << 4) | (15 << 8);
+  if (ntiles >= 2) __builtin_amdgcn_s_waitcnt(kVm2);
+  else if (ntiles == 1) __builtin_amdgcn_s_waitcnt(kVm1);
+  else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  // Q fragments (B operand of S^T = K Q^T): query qi, d = 16 ks + 8 half .. +8.
+  bf16x8 qf[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) {
+    qf[ks] = ld_bf16x8(qbuf + k_off(l32, 2 * ks + half));
+    if (!q_ok) qf[ks] = bf16x8{};
+  }
 
   // The tile loop is unrolled by the stage count so that every LDS reference
   // is to a fixed __shared__ object.
