@@ -27,6 +27,7 @@ for _p in (ROOT, ROOT / "wam-egale_amd"):
 
 METRIC = "DiT-block tokens/sec + µs/layer (dim3072 bf16, 1 GPU); % of MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 STAGE_FFN1 = 12
 
@@ -51,18 +52,46 @@ def build_block(shape, dev, seed=0):
     return blk
 
 
-def timed_steps(fn, steps, warmup):
+class OutputMismatch(RuntimeError):
+    pass
+
+
+def timed_steps(fn, steps, warmup, gate=None):
+    """Average ms per call of fn over `steps` calls after `warmup` calls.
+
+    gate: a name; then the first call's output is kept and the last timed
+    call's output must equal it byte for byte (the reference's timing harness
+    gates every timed output the same way, 算子研究/tools/time_native.py:93-122)."""
     import torch
-    for _ in range(warmup):
-        fn()
+    first = None
+    for i in range(max(warmup, 1 if gate else 0)):
+        out = fn()
+        if gate and i == 0:
+            first = out.clone()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    last = None
     for _ in range(steps):
-        fn()
+        last = fn()
     end.record()
     torch.cuda.synchronize()
+    if gate is not None and not torch.equal(first, last):
+        raise OutputMismatch(f"{gate}: the last timed output differs from the first call's")
     return start.elapsed_time(end) / steps
+
+
+def cache_state(blocks, name="pos"):
+    """Clones of every pool tensor (k, v, id, mask, is_pred) of the blocks."""
+    return [{k: v.clone() for k, v in b.attn1.attn_caches[name].items()} for b in blocks]
+
+
+def check_cache_state(blocks, before, what, name="pos"):
+    import torch
+    for i, (b, snap) in enumerate(zip(blocks, before)):
+        for k, v in snap.items():
+            if not torch.equal(b.attn1.attn_caches[name][k], v):
+                raise OutputMismatch(f"{what}: layer {i} cache {k} changed during a read-only timed run")
 
 
 def stage_times(lib, call, n_calls, mask):
@@ -85,41 +114,87 @@ def stage_times(lib, call, n_calls, mask):
         lib.wam_timer_destroy(timer)
 
 
-def cpu_baseline(shape, seconds_budget=30.0):
-    """The oracle (CPU fp32 restatement of the reference block) on one L4680
-    layer, timed on this host's cores."""
-    import torch
-    from oracle.block import block_forward
-    from wam_ops import synthetic
-    threads = torch.get_num_threads()
-    params = synthetic.block_params(shape, seed=0, device="cpu")
-    params = {k: v.float() for k, v in params.items()}
-    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4680, (6, 26, 30), context_len=512, seed=1)
-    x, ctx = x.float(), ctx.float()
-    with torch.no_grad():
-        t0 = time.perf_counter()
-        block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)  # warmup
-        first = time.perf_counter() - t0
-        runs = max(1, min(3, int(seconds_budget / max(first, 1e-3)) - 1))
-        times = []
-        for _ in range(runs):
-            t0 = time.perf_counter()
-            block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
-            times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    cpu_model = ""
+def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": 4680 / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"one L4680 layer (B=1, 4680 tokens, dim 3072, fp32) through the CPU "
-                      f"oracle, median of {runs} after 1 warmup; {med * 1e3:.0f} ms/layer; "
-                      f"torch threads {threads}, os.cpu_count {os.cpu_count()}, {cpu_model}"}
+    return ""
+
+
+def _time_oracle(params, x, ctx, temb, freqs, heads, eps, warmup, runs):
+    import torch
+    from oracle.block import block_forward
+    with torch.no_grad():
+        for _ in range(warmup):
+            block_forward(params, x, ctx, temb, freqs, heads, eps)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            block_forward(params, x, ctx, temb, freqs, heads, eps)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], times
+
+
+def cpu_baseline(l4680=True):
+    """The oracle (the CPU fp32 restatement of the reference block,
+    WanTransformerBlock.forward, model.py:741-794) timed on this host's cores.
+
+    Main figure: the Wan-1.3B-shaped block (dim 1536, 12 x 128 heads, FFN 8960,
+    B=1, 1024 tokens on a (4, 16, 16) grid, 512 context tokens, per-sample
+    temb), fp32, 3 warmups then the median of 7 runs.  Extra: one L4680 layer
+    (dim 3072, 4680 tokens) in fp32, 1 warmup then the median of 3."""
+    import torch
+    from wam_ops import synthetic
+    threads = torch.get_num_threads()
+    shape = synthetic.WAN_1_3B
+    params = {k: v.float() for k, v in synthetic.block_params(shape, seed=0, device="cpu").items()}
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 1024, (4, 16, 16), context_len=512, seed=0)
+    x, ctx = x.float(), ctx.float()
+    med, times = _time_oracle(params, x, ctx, temb, freqs, shape.heads, shape.eps, 3, 7)
+    res = {"value": round(1024 / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+           "ms_per_layer": round(med * 1e3, 2),
+           "sample": f"C1: one Wan-1.3B-shaped block (dim 1536, 12x128 heads, FFN 8960, B=1, 1024 tokens, "
+                     f"512 context tokens) in fp32 through the CPU oracle; 3 warmups, median of "
+                     f"{len(times)} runs ({', '.join(f'{t * 1e3:.1f}' for t in times)} ms); torch threads "
+                     f"{threads}, os.cpu_count {os.cpu_count()}, {_cpu_model()}"}
+    if l4680:
+        shape = synthetic.WAN22_5B
+        params = {k: v.float() for k, v in synthetic.block_params(shape, seed=0, device="cpu").items()}
+        x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4680, (6, 26, 30), context_len=512, seed=1)
+        med, times = _time_oracle(params, x.float(), ctx.float(), temb, freqs, shape.heads, shape.eps, 1, 3)
+        res["l4680"] = {"tokens_per_s": round(4680 / med, 1), "ms_per_layer": round(med * 1e3, 1),
+                        "sample": "one L4680 layer (B=1, 4680 tokens, dim 3072, fp32) through the CPU oracle, "
+                                  f"1 warmup, median of {len(times)}"}
+    return res
+
+
+def mfma_peaks(lib, dev, iters=20000, reps=3):
+    """Measured dense MFMA throughput (TFLOP/s) of the probe kernel, best of
+    `reps` launches, for bf16 and fp8 e4m3 in both MFMA shapes."""
+    import torch
+    from wam_ops import _lib
+    from wam_ops.ops import stream_handle
+    sink = torch.empty(2 * torch.cuda.get_device_properties(dev).multi_processor_count * 256,
+                       dtype=torch.float32, device=dev)
+    out = {}
+    for name, kind in (("bf16_32x32x16", _lib.PEAK_BF16_32), ("bf16_16x16x32", _lib.PEAK_BF16_16),
+                       ("fp8_32x32x64", _lib.PEAK_FP8_32), ("fp8_16x16x128", _lib.PEAK_FP8_16)):
+        flop = ctypes.c_double()
+        best = 0.0
+        for _ in range(reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            _lib.check(lib.wam_mfma_peak(kind, iters, ctypes.c_void_p(sink.data_ptr()), sink.numel() * 4,
+                                         ctypes.byref(flop), stream_handle(dev)), "wam_mfma_peak")
+            b.record()
+            torch.cuda.synchronize()
+            best = max(best, flop.value / (a.elapsed_time(b) * 1e-3) / 1e12)
+        out[name] = round(best, 1)
+    return out
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "l4680_ffn1_traffic.md"
@@ -178,7 +253,7 @@ def c4a_attention(shape, dev, steps, warmup, q_tokens=1560, prefix=6240):
     slots = torch.arange(prefix, dtype=torch.int32, device=dev)
     n_hist = torch.tensor([prefix], dtype=torch.int32, device=dev)
     ms = timed_steps(lambda: ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n_hist),
-                     steps, warmup)
+                     steps, warmup, gate="C4a self attention")
     return _unit(ms, 4 * q_tokens * (prefix + q_tokens) * shape.dim)
 
 
@@ -209,7 +284,9 @@ def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup,
     def run():
         with torch.no_grad():
             return stack(x, ctx, temb, freqs, candidate_cache_rows=rows)
-    ms = timed_steps(run, steps, warmup)
+    before = cache_state(blocks)
+    ms = timed_steps(run, steps, warmup, gate="stack30")
+    check_cache_state(blocks, before, "stack30")
     g, a = layer_flops(Mv, shape.dim, shape.ffn, ctx.shape[1], self_keys=prefix + Mv, batch=B)
     res = {"layers": layers, "ms_per_forward": round(ms, 3), "us_per_layer": round(ms * 1e3 / layers, 1),
            "tokens_per_s": round(B * Mv / (ms * 1e-3), 1),
@@ -244,8 +321,9 @@ def verify_stack30(shape, dev, x, ctx, temb, freqs, rows, prefix, steps, warmup,
             ops.rope_freqs(grid)
             te, _ = fr["cond"].time(inp["timesteps"], xe.dtype)
             return whole.head(xe, te, False)
-        mms = timed_steps(model_step, steps, warmup)
-        ims = timed_steps(io_step, steps, warmup)
+        mms = timed_steps(model_step, steps, warmup, gate="model30")
+        ims = timed_steps(io_step, steps, warmup, gate="model30 I/O")
+    check_cache_state(blocks, before, "model30")
     res_model = {"ms_per_forward": round(mms, 3), "tokens_per_s": round(B * Mv / (mms * 1e-3), 1),
                  "io_us": round(ims * 1e3, 1), "prepare_text_ms": round(prep_ms, 3),
                  "latents": list(lat.shape), "text": [B, ctx.shape[1], 4096], "timesteps": [B, frames]}
@@ -295,12 +373,14 @@ def main():
         with torch.no_grad():
             return layer(x, ctx, temb, freqs, timer=timer)
 
-    ms = timed_steps(step, args.steps, args.warmup)
+    ms = timed_steps(step, args.steps, args.warmup, gate="L4680")
     # Dominant kernel (FFN1 GEMM + GELU): HIP events around its launch on the
     # launch stream, over the same number of steps.
     ffn1 = stage_times(lib, step, args.steps, 1 << STAGE_FFN1)["ffn1"]
     stages = stage_times(lib, step, 3, (1 << len(_lib.STAGES)) - 1)
 
+    peaks = mfma_peaks(lib, dev)
+    peak_meas = peaks["bf16_32x32x16"]
     gemm, attn = layer_flops(M, D, F, Lc, self_keys=M)
     flops = gemm + attn
     ffn1_flops = 2 * M * D * F
@@ -321,11 +401,18 @@ def main():
                    "tokens": M, "dim": D, "heads": shape.heads, "ffn": F, "context": Lc},
         "layer_tflops": round(layer_tflops, 1),
         "layer_frac_of_bf16_peak": round(layer_tflops / PEAK_BF16_TFLOPS, 4),
+        "layer_frac_of_measured_bf16_peak": round(layer_tflops / peak_meas, 4),
         "layer_flop": flops,
         "roofline": {"bound": "mfma", "kernel": "FFN1 GEMM 4680x14336x3072 + bias + GELU(tanh)",
                      "achieved": round(ffn1_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
-                     "kernel_us": round(ffn1 * 1e3, 1)},
+                     "kernel_us": round(ffn1 * 1e3, 1),
+                     "peak_measured": peak_meas,
+                     "frac_of_measured": round(ffn1_tflops / peak_meas, 4)},
+        "mfma_peak_tflops": {"vendor": {"bf16": PEAK_BF16_TFLOPS, "fp8": PEAK_FP8_TFLOPS},
+                             "measured": peaks},
+        "outputs_checked": "every timed loop's last output equals its first call's byte for byte; "
+                           "read-only KV pools unchanged",
         "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
     }
     # Per-unit lines of the same run (algorithmic FLOP as in the layer count):
@@ -348,7 +435,7 @@ def main():
     def fstep(timer=None):
         with torch.no_grad():
             return flayer(x, ctx, temb, freqs, timer=timer)
-    fms = timed_steps(fstep, args.steps, args.warmup)
+    fms = timed_steps(fstep, args.steps, args.warmup, gate="L4680 fp8 FFN")
     fst = stage_times(lib, fstep, 3, (1 << len(_lib.STAGES)) - 1)
     ffn_flops = 2 * 2 * M * D * F
     out["fp8_ffn_variant"] = {
@@ -376,7 +463,9 @@ def main():
                 return vlayer(xv, ctxv, tembv, freqv, candidate_cache_rows=rows)
         # candidate_cache_rows are read back and validated on the host the first time this
         # tensor is seen (again after any in-place write), as the reference checks them
-        vms = timed_steps(vstep, args.steps, args.warmup)
+        vbefore = cache_state([blk])
+        vms = timed_steps(vstep, args.steps, args.warmup, gate="Lverify")
+        check_cache_state([blk], vbefore, "Lverify")
         g, a = layer_flops(Mv, D, F, Lc, self_keys=prefix + Mv, batch=B)
         out["lverify"] = {"tokens": B * Mv, "us_per_layer": round(vms * 1e3, 1),
                           "tokens_per_s": round(B * Mv / (vms * 1e-3), 1),
@@ -387,7 +476,7 @@ def main():
         out["lverify"]["stack30"], out["lverify"]["model30"] = verify_stack30(
             shape, dev, xv, ctxv, tembv, freqv, rows, prefix, min(args.steps, 5), 2)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(shape)
+        out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
 
 

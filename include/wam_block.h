@@ -390,6 +390,21 @@ void wam_timer_reset(void* timer);
 int wam_timer_read(void* timer, int32_t* stages, float* ms, int max);
 void wam_timer_destroy(void* timer);
 
+/* ------------------------------------------------------------ measurement */
+/* MFMA throughput probe (no counterpart in the reference: it measures the
+ * roofline denominators that the benchmark reports beside the vendor peaks).
+ * Launches one kernel on `stream` in which every wave issues `iters` rounds of
+ * independent MFMAs of the given kind (two waves per SIMD on every CU) and
+ * stores one float per thread to `sink` (2 x CUs x 256 floats).  *flop is the
+ * kernel's FLOP count; time it with events on the same stream. */
+enum {
+  WAM_PEAK_BF16_32 = 0, /* v_mfma_f32_32x32x16_bf16 */
+  WAM_PEAK_BF16_16 = 1, /* v_mfma_f32_16x16x32_bf16 */
+  WAM_PEAK_FP8_32 = 2,  /* v_mfma_scale_f32_32x32x64_f8f6f4, e4m3 x e4m3, unit scales */
+  WAM_PEAK_FP8_16 = 3   /* v_mfma_scale_f32_16x16x128_f8f6f4, e4m3 x e4m3, unit scales */
+};
+int wam_mfma_peak(int kind, int iters, void* sink, int64_t sink_bytes, double* flop, void* stream);
+
 /* ---------------------------------------------------------------- misc */
 const char* wam_last_error(void);
 int wam_abi_version(void);

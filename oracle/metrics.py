@@ -19,8 +19,15 @@ def compare(actual, expected):
     }
 
 
+# Every assert_close call of a test session: (what, max_abs, bound, cosine,
+# cosine bound).  tests/conftest.py prints it at the end of the session, so a
+# run's log shows how much of each tolerance the results use.
+RECORD = []
+
+
 def assert_close(actual, expected, max_abs, min_cos=0.9999, what=""):
     m = compare(actual, expected)
+    RECORD.append((what, m["max_abs"], max_abs, m["cosine"], min_cos))
     ok = m["finite"] and m["max_abs"] <= max_abs and m["cosine"] >= min_cos
     assert ok, f"{what}: {m} (bound max_abs<={max_abs}, cosine>={min_cos})"
     return m

@@ -212,3 +212,58 @@ def test_grad_mode_rejected(dev):
     x, ctx, temb, freqs = _inputs(shape, 1, (1, 2, 3), 8, 2)
     with pytest.raises(RuntimeError, match="inference-only"):
         blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+
+
+def test_inputs_and_weights_unchanged(dev):
+    """A block call never writes its inputs or parameters (the reference's
+    harness asserts inputs_unchanged and weights_unchanged on every native
+    call, 算子研究/tools/verify_native.py:130-134): x, context, temb, the
+    RoPE table and all 27 parameters are byte-identical after calls with
+    update_cache 2, 1 and 0, with debug output, and through WholeLayerBlock
+    with precomputed cross K/V."""
+    from wam_ops import synthetic
+    from wam_ops.native import NativeBlock
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = _shape(**TINY)
+    params = synthetic.block_params(shape, seed=21)
+    blk = native_block(params, shape, dev)
+    blk.attn1.init_kv_cache("pos", 150, shape.heads, shape.head_dim, dev, torch.bfloat16, 1)
+    x, ctx, temb, freqs = (t.to(dev) for t in _inputs(shape, 1, (2, 5, 6), 16, 22))
+    inputs = {"x": x, "context": ctx, "temb": temb, "freqs": freqs}
+    before = {k: v.clone() for k, v in inputs.items()}
+    wbefore = {n: p.detach().clone() for n, p in blk.named_parameters()}
+    rng_cpu, rng_gpu = torch.get_rng_state(), torch.cuda.get_rng_state(dev)
+    with torch.no_grad():
+        for upd in (2, 1, 0):
+            blk(x, ctx, temb, freqs, update_cache=upd)
+        NativeBlock(blk)(x, ctx, temb, freqs, update_cache=0, debug=True)
+        wl = WholeLayerBlock(blk)
+        wl.prepare_context(ctx, precompute=True)
+        wl(x, ctx, temb, freqs, update_cache=0)
+    torch.cuda.synchronize()
+    for k, v in inputs.items():
+        assert torch.equal(v, before[k]), f"input {k} changed"
+    for n, p in blk.named_parameters():
+        assert torch.equal(p.detach(), wbefore[n]), f"parameter {n} changed"
+    assert torch.equal(torch.get_rng_state(), rng_cpu) and torch.equal(torch.cuda.get_rng_state(dev), rng_gpu)
+
+
+def test_prepared_context_batch_checked(dev):
+    """A prepared context fixes the batch: a call with another batch is refused
+    before anything launches."""
+    from wam_ops import synthetic
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = _shape(**TINY)
+    blk = native_block(synthetic.block_params(shape, seed=23), shape, dev)
+    x, ctx, temb, freqs = (t.to(dev) for t in _inputs(shape, 2, (2, 3, 5), 16, 24))
+    ctx2 = ctx[:1].expand(2, -1, -1).contiguous()
+    wl = WholeLayerBlock(blk)
+    with torch.no_grad():
+        wl.prepare_context(ctx2, precompute=True)
+        wl(x, ctx2, temb, freqs)
+        x3 = torch.cat([x, x[:1]])
+        temb3 = torch.cat([temb, temb[:1]])
+        with pytest.raises(RuntimeError, match="prepared"):
+            wl(x3, ctx2, temb3, freqs)
+        with pytest.raises(RuntimeError, match="prepared"):
+            wl(x, ctx2[:1], temb, freqs)

@@ -90,3 +90,23 @@ def test_stack_contract_errors(dev):
             stack(*args, candidate_cache_rows=torch.tensor([0, 1], device=dev, dtype=torch.int32))
     with pytest.raises(RuntimeError, match="inference-only"):
         stack(*args, candidate_cache_rows=torch.tensor([0, 1], device=dev))
+
+
+def test_stack_under_inference_mode(dev):
+    """The verify forward under torch.inference_mode (inference tensors carry
+    no version counter) gives the same output as under no_grad."""
+    from wam_ops import BlockStack
+    shape, params, blocks, ocaches, (x, ctx, temb, freqs) = _setup(dev, n_layers=2, B=3)
+    stack = BlockStack(blocks)
+    args = (x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+    with torch.no_grad():
+        stack.prepare_context(args[1])
+        ref = stack(*args, candidate_cache_rows=torch.tensor([1, 0, 1], device=dev))
+    with torch.inference_mode():
+        rows = torch.tensor([1, 0, 1], device=dev)
+        assert rows.is_inference()
+        out = stack(*args, candidate_cache_rows=rows)
+        out2 = stack(*args, candidate_cache_rows=rows)
+        with pytest.raises(ValueError):
+            stack(*args, candidate_cache_rows=torch.tensor([0, 2, 0], device=dev))
+    assert torch.equal(out, ref) and torch.equal(out2, ref)

@@ -13,7 +13,6 @@
 // (baseline/csrc/block.cu:119-129), the gated residual
 // x + y * gate (block.cu:90-102, gate 2 and 5) and the plain bf16 residual
 // add of cross attention (model.py:783).
-#include <stdlib.h>
 #include <string.h>
 #include "wam_common.h"
 
@@ -51,8 +50,8 @@ struct GemmCfg {
   // the later parts have most of a k-step to land before the next barrier.
   static constexpr int SPLIT = SPLIT_;
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
-  static constexpr int SCHED = SCHED_;    // 1: alternate DS reads and MFMAs; 2: all reads of
-                                          // the next k-step, then this step's MFMAs
+  static constexpr int SCHED = SCHED_;    // 2: all DS reads of the next k-step, then this
+                                          // step's MFMAs; 0: the compiler's order
   static constexpr int kWaves = WGM * WGN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -373,15 +372,7 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
           for (int i = 0; i < C::TM; ++i)
             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks & 1][j], fa[ks & 1][i], acc[j][i],
                                                                 0, 0, 0);
-        if constexpr (C::SCHED == 1) {
-#pragma unroll
-          for (int q = 0; q < (R < MF ? R : MF); ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-          }
-          if constexpr (R < MF) __builtin_amdgcn_sched_group_barrier(0x008, MF - R, 0);
-          else if constexpr (R > MF) __builtin_amdgcn_sched_group_barrier(0x100, R - MF, 0);
-        } else if constexpr (C::SCHED == 2) {
+        if constexpr (C::SCHED == 2) {
           __builtin_amdgcn_sched_group_barrier(0x100, R, 0);   // all DS reads of step ks+1
           __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);  // then the MFMAs of step ks
         }
@@ -506,19 +497,16 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 }
 
 // Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
-using Cfg256x256w8 = GemmCfg<256, 256, 64, 2, 4, 2>;
+// 256x256: one workgroup per CU, the DS reads of a k-step grouped before its
+// MFMAs, loads issued in two parts.  The smaller tiles serve grids that would
+// not cover the chip with 256x256 tiles and the 128x128 tails.
+using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
 using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
 using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
-using Cfg256x256w8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 1>;
-using Cfg256x256w8t = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2>;
-using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
-using Cfg256x256k32w8t4 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2>;
-using Cfg256x128k32w4b2s = GemmCfg<256, 128, 32, 2, 2, 3, 2, 1>;
 // fp8 e4m3 weights (64-byte LDS weight rows, two stages, loads issued in
 // two parts)
 using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 1, 2>;
 using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
-using Cfg256x256k32w8t4s2 = GemmCfg<256, 256, 32, 2, 4, 4, 1, 2, 2, 2>;
 
 // Sum of the k_split fp32 partial ranges of a split-K launch (in range
 // order), then the launch's epilogue.  One thread per 4 consecutive outputs.
@@ -605,22 +593,6 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
       break;
   }
   WAM_LAUNCHED("gemm_bf16_kernel");
-  return WAM_OK;
-}
-
-// Configuration by name (tuning override through WAM_GEMM_CFG), else by shape.
-static int launch_by_name(const char* name, LinearParams& p, hipStream_t s, bool* found) {
-  *found = true;
-  if (!strcmp(name, "256x256w8")) return launch_gemm<Cfg256x256w8>(p, s);
-  if (!strcmp(name, "256x128w4")) return launch_gemm<Cfg256x128w4>(p, s);
-  if (!strcmp(name, "128x128w4")) return launch_gemm<Cfg128x128w4>(p, s);
-  if (!strcmp(name, "256x256w8s")) return launch_gemm<Cfg256x256w8s>(p, s);
-  if (!strcmp(name, "256x256w8t")) return launch_gemm<Cfg256x256w8t>(p, s);
-  if (!strcmp(name, "256x256w8t2")) return launch_gemm<Cfg256x256w8t2>(p, s);
-  if (!strcmp(name, "256x256k32w8t4")) return launch_gemm<Cfg256x256k32w8t4>(p, s);
-  if (!strcmp(name, "256x128k32w4b2s")) return launch_gemm<Cfg256x128k32w4b2s>(p, s);
-  if (!strcmp(name, "256x256k32w8t4s2")) return launch_gemm<Cfg256x256k32w8t4s2>(p, s);
-  *found = false;
   return WAM_OK;
 }
 
@@ -768,13 +740,6 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   if (f8) {
     if (big) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, ws_bytes, s);
     return launch_gemm<Cfg128x128f8>(p, s);
-  }
-  const char* force = getenv("WAM_GEMM_CFG");
-  if (force && *force) {
-    bool found = false;
-    const int rc = launch_by_name(force, p, s, &found);
-    WAM_REQUIRE(found, "wam_linear: unknown WAM_GEMM_CFG '%s'", force);
-    return rc;
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
   if (big) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);

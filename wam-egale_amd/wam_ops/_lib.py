@@ -18,6 +18,7 @@ WAM_OK, WAM_ERR_ARG, WAM_ERR_HIP, WAM_ERR_STATE = 0, -1, -2, -3
 WAM_BF16, WAM_F32, WAM_FP8, WAM_I64, WAM_F64 = 0, 1, 2, 3, 4
 WAM_ACT_NONE, WAM_ACT_SILU = 0, 1
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATE_RES, EPI_BIAS_RES = 0, 1, 2, 3
+PEAK_BF16_32, PEAK_BF16_16, PEAK_FP8_32, PEAK_FP8_16 = 0, 1, 2, 3
 DEBUG_SLOTS = 16
 STAGES = ("ln1", "qkv", "rms_rope", "kv_layout", "self_attn", "self_out", "ln2",
           "cross_q", "cross_kv", "cross_attn", "cross_out", "ln3", "ffn1", "ffn2",
@@ -152,6 +153,7 @@ SIGNATURES = {
     "wam_timestep_embedding": (c_int, [POINTER(TimestepArgs), c_void_p]),
     "wam_rows_linear": (c_int, [POINTER(RowsLinearArgs), c_void_p]),
     "wam_rope_freqs": (c_int, [POINTER(RopeFreqArgs), c_void_p]),
+    "wam_mfma_peak": (c_int, [c_int, c_int, c_void_p, c_int64, POINTER(c_double), c_void_p]),
     "wam_timer_create": (c_void_p, [c_int, c_uint32]),
     "wam_timer_reset": (None, [c_void_p]),
     "wam_timer_read": (c_int, [c_void_p, POINTER(c_int32), POINTER(c_float), c_int]),

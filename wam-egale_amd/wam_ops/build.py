@@ -13,7 +13,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG.parent / "csrc"
-SOURCES = ["block.hip", "gemm.hip", "norm.hip", "attention.hip", "kv_cache.hip", "dit_io.hip"]
+SOURCES = ["block.hip", "gemm.hip", "norm.hip", "attention.hip", "kv_cache.hip", "dit_io.hip", "probe.hip"]
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          # Packed-FP32 VALU ops are disabled for all device code on this target.

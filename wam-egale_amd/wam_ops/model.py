@@ -251,6 +251,7 @@ class WholeModel:
         for layer in self.stack.layers:
             layer.context_rows = layer.context_roots = None
             layer.context_kv = []
+            layer.context_batch = None
 
     # ------------------------------------------------------------ forward
     def embed(self, latents, action_mode):

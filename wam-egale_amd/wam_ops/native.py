@@ -83,7 +83,9 @@ class BoundWeights:
 # Candidate-row tensors already validated: id -> (weakref, torch version
 # counter, batch, pool batch, device).  The same tensor object, unmodified
 # since (its version counter moves with every in-place torch write), passes
-# again without reading it back to the host.
+# again without reading it back to the host.  Inference tensors (created
+# under torch.inference_mode) have no version counter, so they are checked on
+# every call.
 _validated_rows = {}
 
 
@@ -94,12 +96,15 @@ def validate_candidate_rows(rows, batch, pool_batch, device):
     if (rows.ndim != 1 or rows.numel() != batch or rows.dtype != torch.long
             or rows.device != device):
         raise ValueError("invalid candidate_cache_rows for this KV cache")
-    key = (rows._version, batch, pool_batch, device)
-    hit = _validated_rows.get(id(rows))
-    if hit is not None and hit[0]() is rows and hit[1] == key:
-        return
+    key = None if rows.is_inference() else (rows._version, batch, pool_batch, device)
+    if key is not None:
+        hit = _validated_rows.get(id(rows))
+        if hit is not None and hit[0]() is rows and hit[1] == key:
+            return
     if not bool(((rows >= 0) & (rows < pool_batch)).all()):
         raise ValueError("invalid candidate_cache_rows for this KV cache")
+    if key is None:
+        return
     if len(_validated_rows) > 64:
         _validated_rows.clear()
     _validated_rows[id(rows)] = (weakref.ref(rows), key)

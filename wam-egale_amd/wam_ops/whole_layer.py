@@ -28,6 +28,7 @@ class WholeLayerBlock:
         self.eps = block_eps(block)
         self.context_rows = self.context_roots = None
         self.context_kv = []
+        self.context_batch = None
         self._bound = None
 
     def bound(self):
@@ -43,6 +44,7 @@ class WholeLayerBlock:
         self.context_rows = self.context_roots = None
         self.context_kv = []
         batch = context.shape[0]
+        self.context_batch = batch
         bits = context.detach().contiguous().view(torch.uint8).reshape(batch, -1)
         roots, rows = [], []
         for r in range(batch):
@@ -76,6 +78,17 @@ class WholeLayerBlock:
         cache = caches.get(cache_name)
         ctx = encoder_hidden_states
         rows = self.context_rows
+        if self.context_batch is not None:
+            # The prepared grouping maps hidden_states row b to a context row:
+            # both batches must be the one prepare_context saw, or the kernels
+            # would index past the prepared rows.
+            if encoder_hidden_states.shape[0] != self.context_batch:
+                raise RuntimeError(f"context batch {encoder_hidden_states.shape[0]} differs from the "
+                                   f"{self.context_batch} rows prepared by prepare_context")
+            if (rows is not None or self.context_kv) and hidden_states.shape[0] != self.context_batch \
+                    and not (self.context_batch == 1 and rows is None):
+                raise RuntimeError(f"hidden_states batch {hidden_states.shape[0]} does not match the "
+                                   f"{self.context_batch} prepared context rows")
         cross_kv = None
         if self.context_kv:
             cross_kv = self.context_kv
