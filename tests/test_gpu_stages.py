@@ -94,6 +94,12 @@ def test_linear_epilogues(dev, M, K, N):
                    tokens=tokens, gate_index=5)
     r = res.float() + ref * gate
     assert_close(y, r, _ulp_bound(r), 0.99999, "gated residual per-token")
+    # fp32 residual stream, per-token gate, bf16 output (the FFN2 epilogue of
+    # the block with a per-token temb)
+    y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_GATE_RES, residual=res32, table=table, temb=tembt,
+                   tokens=tokens, gate_index=5)
+    r = res32 + ref * gate
+    assert_close(y, r, _ulp_bound(r), 0.99999, "gated fp32 residual per-token")
 
 
 def test_linear_rejects_bad_shapes(dev):

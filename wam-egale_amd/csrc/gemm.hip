@@ -14,6 +14,7 @@
 // x + y * gate (block.cu:90-102, gate 2 and 5) and the plain bf16 residual
 // add of cross attention (model.py:783).
 #include <string.h>
+#include <type_traits>
 #include "wam_common.h"
 
 namespace wam {
@@ -44,6 +45,7 @@ template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
   static constexpr int WB = WB_;          // bytes per weight element: 2 (bf16) or 1 (fp8 e4m3)
+  static constexpr bool kW4 = false;
   // SPLIT > 1: a stage's loads are issued in SPLIT parts, one at the barrier
   // and the others before the MFMAs of the next k-step's first sub-steps, so
   // the load issue does not stall the waves all at once.  With two stages
@@ -496,6 +498,356 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 #undef WAM_GEMM_BUF
 }
 
+// ---------------------------------------------------------------------------
+// 256x256x64 tiles on four waves, one per SIMD.  Each wave owns a 128x128
+// quarter of the tile (16 accumulators of 32x32, held in AGPRs), so a k-step
+// reads 128 KB of MFMA operands from LDS; eight 128x64 waves read 192 KB.
+// Global loads are staged through VGPRs in two register sets (the data of
+// k-step d lives in set d % 2): during k-step t, set (t+1) % 2 is written to
+// the free LDS stage and then reloaded with k-step t+3, so every load has
+// about two k-steps to land.  The loads and the LDS writes are spread evenly
+// over the k-step, about one per three MFMAs: issued in bursts, they fill the
+// texture unit's address and command queues, and a wave that cannot issue a
+// load cannot issue the MFMAs behind it either (4680x3072x14336:
+// SQ_VMEM_TA_ADDR_FIFO_FULL 1.7e7 -> 4.5e5 cycles, k loop 369 -> 337 us).
+struct CfgW4 {
+  static constexpr int BM = 256, BN = 256, BK = 64, WB = 2, kThreads = 256;
+  static constexpr bool kW4 = true;
+};
+
+// The 16 MFMAs of one 16-deep sub-step with the 8 fragment reads of the next
+// sub-step (one after every second MFMA), W LDS writes and V global loads
+// spread evenly between them.
+template <int W, int V>
+__device__ __forceinline__ void w4_sched() {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                   // MFMA
+    if (q & 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // DS read
+    if ((q * W) / 16 != ((q + 1) * W) / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    if ((q * V) / 16 != ((q + 1) * V) / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+  }
+}
+
+// RF32 / OF32: the residual / output is fp32 (else bf16); compile-time so
+// that the epilogue's loads and stores are branch-free.
+template <int EPI, int RF32, int OF32>
+__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
+  __shared__ __attribute__((aligned(1024))) char L0[65536];
+  __shared__ __attribute__((aligned(1024))) char L1[65536];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  // Tile order: XCD-contiguous ranges, then groups of 8 m-tiles swept along n.
+  int tile = xcd_remap(blockIdx.x, gridDim.x);
+  int kp = 0;
+  if constexpr (EPI == kEpiPartial) {
+    const int tiles = p.m_tiles * p.n_tiles;
+    kp = __builtin_amdgcn_readfirstlane(tile / tiles);
+    tile -= kp * tiles;
+  }
+  constexpr int G = 8;
+  const int per_group = G * p.n_tiles;
+  const int group = tile / per_group, in_group = tile - group * per_group;
+  const int first_m = group * G;
+  const int gsize = min(p.m_tiles - first_m, G);
+  const int tm = __builtin_amdgcn_readfirstlane(first_m + in_group % gsize);
+  const int tn = __builtin_amdgcn_readfirstlane(in_group / gsize);
+  const int seg = __builtin_amdgcn_readfirstlane(tn / p.n_tiles_per_seg);
+  const int n0 = (tn - seg * p.n_tiles_per_seg) * 256;
+  const int m0 = tm * 256;
+
+  int nk = p.K / 64, kb = 0;
+  if constexpr (EPI == kEpiPartial) {
+    kb = (int)((int64_t)kp * nk / p.k_split);
+    nk = (int)((int64_t)(kp + 1) * nk / p.k_split) - kb;
+  }
+  // Buffer resources that move to k-tile kt: rows past M (A) or past the
+  // segment's N (W) load as zeros through the bound.
+  const char* wseg = static_cast<const char*>(seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]));
+  const char* abase = reinterpret_cast<const char*>(p.a + (int64_t)m0 * p.lda) + kb * 128;
+  const char* bbase = wseg + (int64_t)n0 * p.ldw * 2 + kb * 128;
+  const uint32_t abytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u - (uint32_t)kb * 128u;
+  const uint32_t bbytes = (uint32_t)min(256, p.seg_n - n0) * (uint32_t)p.ldw * 2u - (uint32_t)kb * 128u;
+  auto res_a = [&](int kt) { return make_rsrc(abase + kt * 128, abytes - (uint32_t)kt * 128u); };
+  auto res_b = [&](int kt) { return make_rsrc(bbase + kt * 128, bbytes - (uint32_t)kt * 128u); };
+
+  // Staging: load i (0..15) of a thread is row 32 (i & 7) + tid / 8 of A
+  // (i < 8) or W (i >= 8), 16-byte chunk tid % 8.  Its LDS slot is that row's
+  // chunk under the swizzle; (row >> 1) & 7 does not depend on i.
+  const int lr = tid >> 3, lc = tid & 7;
+  const int va = lr * (int)p.lda * 2 + lc * 16, vb = lr * (int)p.ldw * 2 + lc * 16;
+  const int ra32 = 32 * (int)p.lda * 2, rb32 = 32 * (int)p.ldw * 2;
+  const int wofs = lds_off<8>(lr, lc);
+  typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
+  u32x4s S0[16], S1[16];
+  auto gload = [&](u32x4s* S, int kt, auto lo_c, auto hi_c) {
+    constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+    const __amdgpu_buffer_rsrc_t ra = res_a(kt), rb = res_b(kt);
+#pragma unroll
+    for (int i = LO; i < HI; ++i) {
+      if (i < 8) S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(ra, va + i * ra32, 0, 0));
+      else S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(rb, vb + (i - 8) * rb32, 0, 0));
+    }
+  };
+  auto swrite = [&](u32x4s* S, char* buf, auto lo_c, auto hi_c) {
+    constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
+#pragma unroll
+    for (int i = LO; i < HI; ++i)
+      *reinterpret_cast<u32x4s*>(buf + (i >= 8 ? 32768 : 0) + (i & 7) * 4096 + wofs) = S[i];
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I5 = std::integral_constant<int, 5>;
+  using I6 = std::integral_constant<int, 6>;
+  using I11 = std::integral_constant<int, 11>;
+  using I16 = std::integral_constant<int, 16>;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = f32x16{};
+  // Fragments of a sub-step: rows wm*128 + 32 i + l32 of A and wn*128 + 32 j
+  // + l32 of W at logical chunk 2 s + half; the swizzle term is (l32 >> 1) & 7.
+  bf16x8 fa[2][4], fb[2][4];
+  const int rowa = (wm * 128 + l32) * 128, rowb = 32768 + (wn * 128 + l32) * 128;
+  auto rd = [&](const char* buf, int s, int f) {
+    const int xo = ((2 * s + half) ^ ((l32 >> 1) & 7)) << 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[f][i] = ld_bf16x8(buf + rowa + i * 4096 + xo);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[f][j] = ld_bf16x8(buf + rowb + j * 4096 + xo);
+  };
+  auto mm = [&](int f) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[f][j], fa[f][i], acc[j][i], 0, 0, 0);
+  };
+
+  // Prologue: k-tiles 0 and 1 into the register sets, k-tile 0 into L0, then
+  // k-tile 2 into set 0.  Loads past the last k-tile repeat it: unconditional
+  // register writes keep the staging sets out of control-flow merges, which
+  // made the register allocator copy and spill them.
+  gload(S0, 0, I0{}, I16{});
+  gload(S1, min(1, nk - 1), I0{}, I16{});
+  swrite(S0, L0, I0{}, I16{});
+  gload(S0, min(2, nk - 1), I0{}, I16{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  rd(L0, 0, 0);
+
+  // One k-step from `cur`; Snext holds k-step t+1 (written to `nxt`) and is
+  // reloaded with k-step t+3.
+  auto kstep = [&](int t, char* cur, char* nxt, u32x4s* Snext) {
+    const int kt3 = min(t + 3, nk - 1);
+    rd(cur, 1, 1);
+    swrite(Snext, nxt, I0{}, I6{});
+    mm(0);
+    w4_sched<6, 0>();
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 2, 0);
+    swrite(Snext, nxt, I6{}, I11{});
+    gload(Snext, kt3, I0{}, I6{});
+    mm(1);
+    w4_sched<5, 6>();
+    __builtin_amdgcn_sched_barrier(0);
+    rd(cur, 3, 1);
+    swrite(Snext, nxt, I11{}, I16{});
+    gload(Snext, kt3, I6{}, I11{});
+    mm(0);
+    w4_sched<5, 5>();
+    __builtin_amdgcn_sched_barrier(0);
+    // Every wave has written its part of the next stage and read its last
+    // fragments of this one.
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    rd(nxt, 0, 0);
+    gload(Snext, kt3, I11{}, I16{});
+    mm(1);
+    w4_sched<0, 5>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Pairs of k-steps without a condition inside (a conditional second step
+  // made the accumulators cross a control-flow merge and spill).
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
+    kstep(t, L0, L1, S1);
+    kstep(t + 1, L1, L0, S0);
+  }
+  if (t < nk) kstep(t, L0, L1, S1);
+
+  // ------------------------------------------------------------- epilogue
+  // Two rounds of 128 rows through both stage buffers (1 KB fp32 rows, 16-byte
+  // chunks XOR-swizzled by row & 15).  In round r every wave writes its
+  // m-tiles 2r and 2r+1 (rows wm*128 + 64 r .. +64 of the tile) as whole
+  // 4-float slices of the accumulators, then every thread reads back one
+  // 16-byte chunk (4 columns) of 32 rows, so bias, gate, residual and output
+  // accesses are whole contiguous rows.  Residual loads and output stores go
+  // through buffer resources bounded at row M: rows past M read zeros and
+  // their stores are dropped, so the epilogue has no per-row branches, and a
+  // round's residual loads are all in flight during its LDS exchange.
+  const int q = tid & 63;
+  const int n = n0 + 4 * q;  // the W4 path takes whole 256-column tiles only
+  float bv[4] = {0.f, 0.f, 0.f, 0.f};
+  {
+    const bf16* __restrict__ bias = seg == 0 ? p.bias[0] : (seg == 1 ? p.bias[1] : p.bias[2]);
+    if (bias) {
+      const bf16x4 tb = *reinterpret_cast<const bf16x4*>(bias + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(tb[e]);
+    }
+  }
+  float gate[4] = {0.f, 0.f, 0.f, 0.f};
+  bool gate_once = false;
+  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + 256, p.M) - 1);
+    if (gate_once) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
+  }
+  constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
+  constexpr bool PART = EPI == kEpiPartial;
+  constexpr int RB = RF32 ? 4 : 2;                 // residual bytes per element
+  constexpr int OB = (OF32 || PART) ? 4 : 2;       // output bytes per element
+  const uint32_t rows_left = (uint32_t)(p.M - m0);
+  // (without a residual the resource is a zero-length one over the output; never read)
+  const __amdgpu_buffer_rsrc_t rres =
+      RES ? make_rsrc(static_cast<const char*>(p.res) + ((int64_t)m0 * p.ldr + n0) * RB,
+                      (uint32_t)((rows_left - 1) * (uint32_t)p.ldr + 256u) * RB)
+          : make_rsrc(p.a, 0u);
+  __amdgpu_buffer_rsrc_t rout;
+  {
+    char* obase;
+    int64_t ld;
+    if constexpr (PART) {
+      obase = reinterpret_cast<char*>(p.part + ((int64_t)kp * p.M + m0) * p.seg_n + n0);
+      ld = p.seg_n;
+    } else {
+      void* out = seg == 0 ? p.out[0] : (seg == 1 ? p.out[1] : p.out[2]);
+      obase = static_cast<char*>(out) + ((int64_t)m0 * p.ldo + n0) * OB;
+      ld = p.ldo;
+    }
+    rout = make_rsrc(obase, (uint32_t)((rows_left - 1) * (uint32_t)ld + 256u) * OB);
+  }
+  const int ld_out = PART ? p.seg_n : (int)p.ldo;
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+  // tile row handled by pass ps (0..31) of round r
+  auto row_of = [&](int r, int ps) {
+    const int rr = ps * 4 + (tid >> 6);
+    return (rr >> 6) * 128 + 64 * r + (rr & 63);
+  };
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    u32x4v rraw[RES ? 32 : 1];
+    if constexpr (RES) {
+#pragma unroll
+      for (int ps = 0; ps < 32; ++ps) {
+        const int off = (row_of(r, ps) * (int)p.ldr + 4 * q) * RB;
+        if constexpr (RF32) {
+          rraw[ps] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0));
+        } else {
+          const u32x2v t2 = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rres, off, 0, 0));
+          rraw[ps] = u32x4v{t2[0], t2[1], 0u, 0u};
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    {
+      char* buf = wm ? L1 : L0;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int i = 2 * r + ii;
+            const int lrw = ii * 32 + l32;
+            const int qq = wn * 32 + j * 8 + 2 * g + half;
+            f32x4 v;
+            if (g == 0) v = __builtin_shufflevector(acc[j][i], acc[j][i], 0, 1, 2, 3);
+            else if (g == 1) v = __builtin_shufflevector(acc[j][i], acc[j][i], 4, 5, 6, 7);
+            else if (g == 2) v = __builtin_shufflevector(acc[j][i], acc[j][i], 8, 9, 10, 11);
+            else v = __builtin_shufflevector(acc[j][i], acc[j][i], 12, 13, 14, 15);
+            *reinterpret_cast<f32x4*>(buf + lrw * 1024 + ((qq ^ (lrw & 15)) << 4)) = v;
+          }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int b8 = 0; b8 < 4; ++b8) {
+      f32x4 vv[8];
+#pragma unroll
+      for (int k8 = 0; k8 < 8; ++k8) {
+        const int ps = b8 * 8 + k8;
+        const int rr = ps * 4 + (tid >> 6);
+        const char* buf = ps < 16 ? L0 : L1;
+        const int lrw = rr & 63;
+        vv[k8] = *reinterpret_cast<const f32x4*>(buf + lrw * 1024 + ((q ^ (lrw & 15)) << 4));
+      }
+#pragma unroll
+      for (int k8 = 0; k8 < 8; ++k8) {
+        const int ps = b8 * 8 + k8;
+        const int row = row_of(r, ps);
+        const int off = (row * ld_out + 4 * q) * OB;
+        if constexpr (PART) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, vv[k8]), rout, off, 0, 0);
+          continue;
+        }
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = vv[k8][e] + bv[e];
+        if constexpr (EPI == WAM_EPI_BIAS_GELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
+        } else if constexpr (RES) {
+          float rv[4];
+          const u32x4v t4 = rraw[ps];
+          if constexpr (RF32) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rv[e] = __uint_as_float(t4[e]);
+          } else {
+            rv[0] = __uint_as_float(t4[0] << 16);
+            rv[1] = __uint_as_float(t4[0] & 0xffff0000u);
+            rv[2] = __uint_as_float(t4[1] << 16);
+            rv[3] = __uint_as_float(t4[1] & 0xffff0000u);
+          }
+          if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+            float gt[4];
+            if (gate_once) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) gt[e] = gate[e];
+            } else {
+              // rows past M read the last row's modulation (their stores are dropped)
+              ld_mod4(p.gate, p.mod_d, min(m0 + row, p.M - 1), p.gate_index, n + p.n_off, gt);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e] * gt[e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
+          }
+        }
+        if constexpr (OF32 && RES) {
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4v{__float_as_uint(y[0]), __float_as_uint(y[1]),
+                                                        __float_as_uint(y[2]), __float_as_uint(y[3])},
+                                                 rout, off, 0, 0);
+        } else {
+          bf16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2v, o), rout, off, 0, 0);
+        }
+      }
+      // one batch of LDS reads live at a time
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 // Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
 // 256x256: one workgroup per CU, the DS reads of a k-step grouped before its
 // MFMAs, loads issued in two parts.  The smaller tiles serve grids that would
@@ -545,9 +897,27 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p)
   epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false, rv);
 }
 
+template <class C, int EPI>
+static void launch_tiles(dim3 grid, const LinearParams& p, hipStream_t s) {
+  if constexpr (C::kW4) {
+    constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
+    if constexpr (RES) {
+      if (p.res_f32 && p.out_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 1>), grid, dim3(C::kThreads), 0, s, p);
+      else if (p.res_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 0>), grid, dim3(C::kThreads), 0, s, p);
+      else if (p.out_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 1>), grid, dim3(C::kThreads), 0, s, p);
+      else hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0>), grid, dim3(C::kThreads), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0>), grid, dim3(C::kThreads), 0, s, p);
+    }
+  } else {
+    hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI>), grid, dim3(C::kThreads), 0, s, p);
+  }
+}
+
 template <class C>
 static int launch_gemm(LinearParams& p, hipStream_t s) {
-  WAM_REQUIRE(p.K % C::BK == 0 && (p.n_seg_count == 1 || p.seg_n % C::BN == 0),
+  WAM_REQUIRE(p.K % C::BK == 0 && (p.n_seg_count == 1 || p.seg_n % C::BN == 0) &&
+              (!C::kW4 || p.seg_n % C::BN == 0),
               "wam_linear: N=%d / K=%d do not fit a %dx%dx%d tile", p.seg_n, p.K, C::BM, C::BN, C::BK);
   p.n_tiles_per_seg = (p.seg_n + C::BN - 1) / C::BN;
   p.m_tiles = (p.M + C::BM - 1) / C::BM;
@@ -555,7 +925,7 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
   const int grid = p.m_tiles * p.n_tiles;
   if (p.k_split > 1) {
     WAM_REQUIRE(p.n_seg_count == 1 && p.part && p.k_split <= p.K / C::BK, "wam_linear: bad split-K launch");
-    hipLaunchKernelGGL((gemm_bf16_kernel<C, kEpiPartial>), dim3(grid * p.k_split), dim3(C::kThreads), 0, s, p);
+    launch_tiles<C, kEpiPartial>(dim3(grid * p.k_split), p, s);
     WAM_LAUNCHED("gemm_bf16_kernel");
     const unsigned rblocks = (unsigned)(((int64_t)p.M * (p.seg_n / 4) + 255) / 256);
     switch (p.epi) {
@@ -580,16 +950,16 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
   }
   switch (p.epi) {
     case WAM_EPI_BIAS:
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, WAM_EPI_BIAS>), dim3(grid), dim3(C::kThreads), 0, s, p);
+      launch_tiles<C, WAM_EPI_BIAS>(dim3(grid), p, s);
       break;
     case WAM_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, WAM_EPI_BIAS_GELU>), dim3(grid), dim3(C::kThreads), 0, s, p);
+      launch_tiles<C, WAM_EPI_BIAS_GELU>(dim3(grid), p, s);
       break;
     case WAM_EPI_BIAS_GATE_RES:
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, WAM_EPI_BIAS_GATE_RES>), dim3(grid), dim3(C::kThreads), 0, s, p);
+      launch_tiles<C, WAM_EPI_BIAS_GATE_RES>(dim3(grid), p, s);
       break;
     default:
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, WAM_EPI_BIAS_RES>), dim3(grid), dim3(C::kThreads), 0, s, p);
+      launch_tiles<C, WAM_EPI_BIAS_RES>(dim3(grid), p, s);
       break;
   }
   WAM_LAUNCHED("gemm_bf16_kernel");
@@ -742,7 +1112,16 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return launch_gemm<Cfg128x128f8>(p, s);
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  if (big) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
+  // The four-wave kernel has the faster k loop; its epilogue reads residual
+  // rows with one wave per SIMD, which costs more than the loop gains when the
+  // loop is short (measured on 4680 and 6240 x 3072 x 3072 with the gated and
+  // plain residual epilogues: 4-12% slower than the eight-wave kernel; every
+  // other block GEMM 0-10% faster).
+  if (big) {
+    const bool res = a->epilogue == WAM_EPI_BIAS_GATE_RES || a->epilogue == WAM_EPI_BIAS_RES;
+    if (res && a->K <= 4096) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
+    return launch_big<CfgW4, Cfg128x128w4>(p, ws_bytes, s);
+  }
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
   if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
   return launch_gemm<Cfg128x128w4>(p, s);
