@@ -209,6 +209,15 @@ typedef struct {
 
 int wam_attention(const wam_attention_args* args, void* stream);
 int64_t wam_attention_workspace_bytes(int B, int Mq, int H, int max_keys);
+/* wam_attention without a workspace, and without any device allocation: no
+ * counterpart in the reference.  For callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc).  args->workspace
+ * must be NULL and workspace_bytes 0; the key-range split's partial results
+ * go to a static 64 MiB device array of the library (one per GPU, held until
+ * the process ends).  A shape whose split needs more than that
+ * (wam_attention_workspace_bytes > 64 MiB) is refused with WAM_ERR_ARG.
+ * Calls that overlap on one GPU share the array and race. */
+int wam_attention_noalloc(const wam_attention_args* args, void* stream);
 
 /* ------------------------------------------------------------- KV pool */
 /* Device-side bookkeeping of the original-mode KV pool (model.py:547-593):

@@ -20,6 +20,7 @@
 // pool rows into a contiguous tensor (pack_kernel,
 // 算子研究/wam_ops/baseline/csrc/block.cu:213-224); here the pool is read in
 // place through the slot list.
+#include <mutex>
 #include "wam_common.h"
 
 namespace wam {
@@ -515,7 +516,68 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   return WAM_OK;
 }
 
+// ------------------------------------------------------------ no allocation
+// wam_attention for callers that cannot allocate device memory (code under
+// HIP graph capture, tight serving loops): the key-range split's partial
+// results go to a file-scope device array instead of a caller workspace.
+// Every GPU the library runs on holds its own copy of the array until the
+// process ends; calls on one GPU share it, so calls that overlap on one GPU
+// race.  Nothing in it needs clearing: every piece of a split writes its whole
+// partial (an empty key range writes m = -inf, l = 0, O = 0) before the
+// combine reads it.
+constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.  The array's name is only a host-side
+// stand-in: kernels get this address.
+static int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  WAM_HIP(hipGetDevice(&dev));
+  WAM_REQUIRE(dev >= 0 && dev < 64, "wam_attention_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    WAM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    WAM_REQUIRE(p != nullptr, "wam_attention_noalloc: no address for the scratch array");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return WAM_OK;
+}
+
+int attention_noalloc(const wam_attention_args* a, hipStream_t s) {
+  WAM_REQUIRE(a != nullptr, "wam_attention_noalloc: null args");
+  WAM_REQUIRE(a->workspace == nullptr && a->workspace_bytes == 0,
+              "wam_attention_noalloc: takes no workspace (the split uses the library's own scratch)");
+  WAM_REQUIRE(a->B >= 1 && a->H >= 1 && a->Mq >= 0 && a->Mk >= 1 && a->max_keys >= 0,
+              "wam_attention_noalloc: bad shape B=%d H=%d Mq=%d Mk=%d", a->B, a->H, a->Mq, a->Mk);
+  // The split wam_attention would run with an unlimited workspace; shapes
+  // whose partial results exceed the scratch are refused, not re-planned, so
+  // that both entry points compute the same thing.
+  const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
+  const int64_t need = a->Mq > 0 ? plan_bytes(attention_plan(a->B, a->Mq, a->H, keys, INT64_MAX)) : 0;
+  WAM_REQUIRE(need <= kNoAllocScratchBytes,
+              "wam_attention_noalloc: this shape's key-range split needs %lld bytes of scratch, more than "
+              "the %lld-byte maximum; call wam_attention with a workspace instead",
+              (long long)need, (long long)kNoAllocScratchBytes);
+  wam_attention_args b = *a;
+  if (need > 0) {
+    void* p = nullptr;
+    WAM_TRY(scratch_address(&p));
+    b.workspace = p;
+    b.workspace_bytes = need;
+  }
+  return attention(&b, s);
+}
+
 }  // namespace wam
+
+extern "C" int wam_attention_noalloc(const wam_attention_args* args, void* stream) {
+  return wam::attention_noalloc(args, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int wam_attention(const wam_attention_args* args, void* stream) {
   return wam::attention(args, static_cast<hipStream_t>(stream));

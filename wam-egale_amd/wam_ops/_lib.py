@@ -143,6 +143,7 @@ SIGNATURES = {
     "wam_ln_modulate": (c_int, [POINTER(LnArgs), c_void_p]),
     "wam_rms_rope": (c_int, [POINTER(RmsRopeArgs), c_void_p]),
     "wam_attention": (c_int, [POINTER(AttentionArgs), c_void_p]),
+    "wam_attention_noalloc": (c_int, [POINTER(AttentionArgs), c_void_p]),
     "wam_kv_layout": (c_int, [POINTER(KvLayoutArgs), c_void_p]),
     "wam_kv_commit": (c_int, [POINTER(KvCommitArgs), c_void_p]),
     "wam_block_workspace_bytes": (c_size_t, [c_int] * 7),
