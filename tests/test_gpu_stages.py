@@ -159,7 +159,12 @@ def _ref_attn(q, k, v):
 
 
 @pytest.mark.parametrize("B,Mq,Mk,H", [(1, 1, 1, 1), (1, 100, 37, 2), (2, 129, 200, 3),
-                                       (1, 4680, 512, 24), (1, 1560, 1560, 24)])
+                                       (1, 4680, 512, 24), (1, 1560, 1560, 24),
+                                       # grids of >= 128 workgroups of 256 queries (the
+                                       # pipelined kernel): ragged queries and keys, one
+                                       # key, key-range splits
+                                       (2, 1000, 77, 16), (1, 3000, 1, 24), (1, 4100, 4099, 24),
+                                       (3, 700, 2500, 24), (1, 4680, 4680, 24)])
 def test_attention_plain(dev, B, Mq, Mk, H):
     from wam_ops import ops
     q = _randn((B, Mq, H, 128), dev, 1)

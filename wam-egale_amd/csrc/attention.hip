@@ -360,6 +360,345 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
   }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined variant for calls whose keys are all this call's own
+// (no KV pool): 8 waves x 32 queries, key tiles of 64 in 3 LDS stages.  Per
+// tile t a wave issues
+//   g1: S(t+1) = K_{t+1} Q^T (16 MFMAs)  interleaved with  softmax of S(t)
+//   g2: O += V_t^T P(t)     (16 MFMAs)
+// so the exponentials, row sums and bf16 packing of one tile run under the
+// MFMAs of the next; in attention_kernel they ran between the wave's own MFMA
+// phases, with both waves of a SIMD in the same phase (MFMA busy 34% on
+// 4680 x 4680).  S(t) and S(t+1) live in two fixed register sets: tiles are
+// processed in pairs, with a peeled last tile.  K/V come in through buffer
+// loads straight to LDS (rows past Mk read zeros) and Q through buffer loads
+// into registers.  Lane layouts of S^T, P and O^T are those of
+// attention_kernel.
+__global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args a, int n_full, int n_split,
+                                                              float* __restrict__ part) {
+  __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, half = lane >> 5;
+  constexpr int QT = 256;
+  const int nqt = (a.Mq + QT - 1) / QT;
+  const int n_tail = nqt * a.H * a.B - n_full;
+  int unit, split = 0, ns = 1;
+  if ((int)blockIdx.x < n_full) {
+    unit = xcd_remap(blockIdx.x, n_full);
+  } else {
+    const int piece = xcd_remap(blockIdx.x - n_full, gridDim.x - n_full);
+    unit = n_full + piece % n_tail;
+    split = piece / n_tail;
+    ns = n_split;
+  }
+  unit = __builtin_amdgcn_readfirstlane(unit);
+  split = __builtin_amdgcn_readfirstlane(split);
+  ns = __builtin_amdgcn_readfirstlane(ns);
+  const int qt = unit % nqt, bh = unit / nqt;
+  const int b = bh % a.B, h = bh / a.B;
+  const int krow = __builtin_amdgcn_readfirstlane(a.kv_rows ? clamp_row((int)a.kv_rows[b], a.kv_batch)
+                                                            : clamp_row(b, a.kv_batch));
+  const int nkt = (a.Mk + kAttnKT - 1) / kAttnKT;
+  const int t_first = (int)((int64_t)split * nkt / ns);
+  const int ntiles = (int)((int64_t)(split + 1) * nkt / ns) - t_first;
+
+  const bf16* kbase = static_cast<const bf16*>(a.k) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
+  const bf16* vbase = static_cast<const bf16*>(a.v) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
+  const uint32_t kv_bytes = (uint32_t)(((int64_t)(a.Mk - 1) * a.kv_rstride + kAttnHD) * 2);
+  const i32x4 rk = make_rsrc4(kbase, kv_bytes), rv = make_rsrc4(vbase, kv_bytes);
+  const bf16* qbase = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride + h * kAttnHD;
+  const __amdgpu_buffer_rsrc_t rq =
+      make_rsrc(qbase, (uint32_t)(((int64_t)(a.Mq - 1) * a.q_rstride + kAttnHD) * 2));
+
+  const int qi = qt * QT + wave * 32 + l32;
+  const bool q_ok = qi < a.Mq;
+  bf16x8 qf[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+    qf[ks] = __builtin_bit_cast(
+        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, (qi * (int)a.q_rstride + 16 * ks + 8 * half) * 2, 0, 0));
+
+  // Direct-to-LDS loads of a tile: wave w fills K and V blocks w and w + 8 (4
+  // keys each); lane L takes key row 4g + L/16 of the tile, physical chunk
+  // L % 16, and fetches the logical chunk the swizzle puts there.  For both
+  // blocks (row & 15) = 4 (w & 3) + L/16 and (row & 3) = L/16.  Keys past Mk
+  // read key Mk - 1 (finite values; their probabilities are zero).  Byte
+  // offsets are 32-bit: the host only picks this kernel when they fit.
+  const int lr = lane >> 4, pch = lane & 15;
+  const int lck = (pch ^ (4 * (wave & 3) + lr)) << 4, lcv = (pch ^ (lr << 2)) << 4;
+  auto issue = [&](int T, int st_bytes) {
+    char* sb = lds + st_bytes;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int g = wave + 8 * i;
+      const int row = min(T * kAttnKT + 4 * g + lr, a.Mk - 1) * (int)a.kv_rstride * 2;
+      asm_ld16_lds(rk, sb + g * 1024, row + lck);
+      asm_ld16_lds(rv, sb + kAttnTile + g * 1024, row + lcv);
+    }
+  };
+  constexpr int kVmTile = 4;  // direct-to-LDS loads per wave per tile
+
+  const float sc = a.scale * kLog2e;
+  const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+  f32x16 s0[2], s1[2];
+  bf16x8 pb[4];
+
+  // Per-lane LDS offsets inside a stage, computed once.  K fragment (kt, ks):
+  // key kt*32 + l32, chunk 2 ks + half under the (key & 15) swizzle, i.e.
+  // kofs[ks] + 8192 kt.  Transposed V fragment (dt, ks), part pt: key 16 ks
+  // + 4 half + 8 pt + (lane % 16) / 4, d = 32 dt + 16 ((lane / 16) % 2) +
+  // 4 (lane % 4); with the V swizzle that is vofs[dt] + 4096 ks + 2048 pt.
+  int kofs[8], vofs[4];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) kofs[ks] = l32 * 256 + (((2 * ks + half) ^ (l32 & 15)) << 4);
+  {
+    const int xs = tr_i >> 2, low = 2 * tr_gh + ((tr_i & 3) >> 1);
+    const int vlane = kAttnTile + (4 * half + xs) * 256 + (low << 4) + 8 * (tr_i & 1);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) vofs[dt] = vlane + 64 * (dt ^ xs);
+  }
+  // S = K Q^T for one tile: K fragments are read two k-steps ahead of their
+  // MFMAs (three rotating sets), so each read has two steps to land.
+  // Stage byte offsets are wave-uniform values kept in scalar registers, so
+  // that each fragment address is one add of a per-lane offset plus a
+  // constant in the instruction's offset field.
+  // The fragment addresses of a stage are formed first, made opaque and
+  // fenced off from what follows, so that the scheduling groups of the MFMA
+  // block below only see the loads, the MFMAs and the softmax.
+  auto s_mfma = [&](int st_bytes, f32x16 (&s)[2]) {
+    const int sb = __builtin_amdgcn_readfirstlane(st_bytes);
+    int ka[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      ka[ks] = sb + kofs[ks];
+      asm volatile("" : "+v"(ka[ks]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+    bf16x8 kf[3][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) kf[ks][kt] = ld_bf16x8(lds + ka[ks] + 8192 * kt);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (ks + 2 < 8) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) kf[(ks + 2) % 3][kt] = ld_bf16x8(lds + ka[ks + 2] + 8192 * kt);
+      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3][kt], qf[ks], s[kt], 0, 0, 0);
+    }
+  };
+  // O += V^T P for one tile: transposed V fragments two MFMAs ahead.
+  auto pv_mfma = [&](int st_bytes) {
+    const int sb = __builtin_amdgcn_readfirstlane(st_bytes);
+    int va4[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      va4[dt] = sb + vofs[dt];
+      asm volatile("" : "+v"(va4[dt]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    auto vload = [&](int i) {
+      const int ks = i >> 2, dt = i & 3;
+      bf16x8 va;
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        const bf16x4 t4 = ld_tr16(lds + va4[dt] + 4096 * ks + 2048 * pt);
+        va[4 * pt + 0] = t4[0]; va[4 * pt + 1] = t4[1];
+        va[4 * pt + 2] = t4[2]; va[4 * pt + 3] = t4[3];
+      }
+      return va;
+    };
+    bf16x8 vf[3];
+    vf[0] = vload(0);
+    vf[1] = vload(1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 2 < 16) vf[(i + 2) % 3] = vload(i + 2);
+      o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[i % 3], pb[i >> 2], o[i & 3], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i + 2 < 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  // Softmax of tile T, without branches so that it can run between the
+  // MFMAs of the next tile: maxima with the NaN-propagating maximum (MFMA
+  // results need no quieting), a lazy running max (log2 units; it only moves
+  // where a tile's max exceeds it by more than 8), probabilities packed to
+  // bf16 and summed from the packed values (dot2 with ones), so the sum is
+  // that of the weights O accumulates.  MASK: the tile may hold keys past Mk
+  // (only the last tile of the key set).  Returns whether the max moved in
+  // any lane; alpha is the factor O must then be scaled by (1 elsewhere).
+  auto softmax = [&](f32x16 (&s)[2], int T, auto mask_tag, float& alpha) -> bool {
+    if constexpr (decltype(mask_tag)::value) {
+      const int valid = a.Mk - T * kAttnKT;
+      // key kt*32 + 8 (v / 4) + 4 half + v % 4 is past the end: compare the
+      // compile-time part against one per-lane threshold
+      const int thr = valid - 4 * half;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (kt * 32 + 8 * (v >> 2) + (v & 3) >= thr) s[kt][v] = -INFINITY;
+    }
+    float mq[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x16& x = s[c >> 1];
+      const int o8 = (c & 1) * 8;
+      float m = __builtin_elementwise_maximum(x[o8], x[o8 + 1]);
+#pragma unroll
+      for (int v = 2; v < 8; v += 2)
+        m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(x[o8 + v], x[o8 + v + 1]));
+      mq[c] = m;
+    }
+    const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mq[0], mq[1]),
+                                                   __builtin_elementwise_maximum(mq[2], mq[3]));
+    const float mt = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64)) * sc;
+    const bool grow = mt > m_run + 8.0f;
+    const float m_new = grow ? mt : m_run;
+    alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kt][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][v], sc, -m_run));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pb[ks][u] = static_cast<bf16>(s[ks >> 1][(ks & 1) * 8 + u]);
+    const bf16x2 ones = {static_cast<bf16>(1.0f), static_cast<bf16>(1.0f)};
+    float ps[2] = {0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x2 w0 = __builtin_bit_cast(u32x2, __builtin_shufflevector(pb[ks], pb[ks], 0, 1, 2, 3)),
+                  w1 = __builtin_bit_cast(u32x2, __builtin_shufflevector(pb[ks], pb[ks], 4, 5, 6, 7));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ps[j & 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, j < 2 ? w0[j] : w1[j - 2]), ones,
+                                                    ps[j & 1], false);
+    }
+    l_run = __builtin_fmaf(l_run, alpha, ps[0] + ps[1]);
+    return __builtin_amdgcn_ballot_w64(grow) != 0;
+  };
+  // The 16 MFMAs of S(t+1) with its K reads (one per MFMA, 12 after the
+  // first 4 issued up front) and the softmax of S(t) between them: the max
+  // reduction under the first four, then exponentials (transcendental group)
+  // and the other VALU work under the rest.
+  auto interleave = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (q < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (q < 4) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x400, 3, 0);  // transcendental
+      }
+    }
+  };
+
+  if (ntiles > 0) {
+    // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
+    // tile 0 has landed.
+    issue(t_first, 0);
+    if (ntiles > 1) issue(t_first + 1, kAttnStage);
+    if (ntiles > 1) __builtin_amdgcn_s_waitcnt((kVmTile & 15) | (7 << 4) | (15 << 8));
+    else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    __builtin_amdgcn_s_barrier();
+    s_mfma(0, s0);
+    // Stages of tiles t, t+1 and t+2, rotated each step (scalar values; an
+    // expression in t would become per-lane induction variables).
+    int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
+    // One step: tile t's softmax under S(t+1) (the last tile's successor is
+    // itself again, computed and discarded), O rescaled where the max moved,
+    // then O += V_t P(t).  Only the last tile is masked.
+    auto step = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
+      const int T = t_first + t;
+      const bool has_next = t + 1 < ntiles;
+      // tile t+1 has landed and every wave is done with the stage of t-1
+      if (has_next) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      __builtin_amdgcn_s_barrier();
+      if (t + 2 < ntiles) issue(T + 2, st2);
+      float alpha;
+      s_mfma(has_next ? st1 : st0, snxt);
+      const bool moved = softmax(scur, T, mask_tag, alpha);
+      interleave();
+      // P(t) is complete here, before the branch below (keeps the
+      // exponentials in this block, between the MFMAs of S(t+1)).
+      asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]));
+      __builtin_amdgcn_sched_barrier(0);
+      if (moved) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      }
+      pv_mfma(st0);
+      __builtin_amdgcn_sched_barrier(0);
+      const int st_done = st0;
+      st0 = st1;
+      st1 = st2;
+      st2 = st_done;
+    };
+    const std::integral_constant<bool, false> full;
+    const std::integral_constant<bool, true> last;
+    const int nm = ntiles - 1;  // tiles before the last one hold no key past Mk
+    int t = 0;
+    for (; t + 1 < nm; t += 2) {
+      step(t, s0, s1, full);
+      step(t + 1, s1, s0, full);
+    }
+    if (t < nm) {
+      step(t, s0, s1, full);
+      step(t + 1, s1, s0, last);
+    } else {
+      step(t, s0, s1, last);
+    }
+  }
+
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (ns > 1) {
+    if (q_ok) {
+      const int64_t row = ((int64_t)split * n_tail + (unit - n_full)) * QT + wave * 32 + l32;
+      float* op = part + row * kAttnHD;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(op + dt * 32 + 8 * g + 4 * half) =
+              make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+      if (half == 0) {
+        float* ml = part + (int64_t)n_split * n_tail * QT * kAttnHD + row * 2;
+        *reinterpret_cast<float2*>(ml) = make_float2(m_run, l);
+      }
+    }
+    return;
+  }
+  const float inv = 1.f / l;
+  if (q_ok) {
+    bf16* op = static_cast<bf16*>(a.o) + (int64_t)b * a.o_bstride + (int64_t)qi * a.o_rstride + h * kAttnHD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 t4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t4[e] = static_cast<bf16>(o[dt][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4*>(op + dt * 32 + 8 * g + 4 * half) = t4;
+      }
+  }
+}
+
 // Merge the n_split partial results of each query row of the split units:
 // O = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with m = max_i m_i.  One
 // wave per (split unit, query) row, two of the 128 outputs per lane; every
@@ -460,6 +799,10 @@ int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
   return plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX));
 }
 
+// Selects the software-pipelined kernel for calls without a KV pool (a switch for
+// side-by-side measurement; always on in the library).
+static bool g_attn_w4 = true;
+
 int attention(const wam_attention_args* a, hipStream_t s) {
   WAM_REQUIRE(a != nullptr, "wam_attention: null args");
   WAM_REQUIRE(a->head_dim == kAttnHD, "wam_attention: head_dim must be 128 (got %d)", a->head_dim);
@@ -492,11 +835,20 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   WAM_REQUIRE(grid8 < (1 << 26), "wam_attention: grid too large");
   const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
   const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0);
+  // Keys of this call only (no KV pool), with every Q and K/V row's byte
+  // offset inside 31 bits: the software-pipelined kernel.
+  const bool own_only = a->n_hist_dev == nullptr && g_attn_w4 &&
+                        ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
+                        ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
   if (p.n_split > 1) {
     float* part = static_cast<float*>(a->workspace);
     const int64_t grid = (int64_t)p.n_full + (int64_t)p.n_tail * p.n_split;
-    hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full,
-                       p.n_split, part);
+    if (own_only)
+      hipLaunchKernelGGL(attention_sp_kernel, dim3((unsigned)grid), dim3(512), 0, s, *a, p.n_full, p.n_split,
+                         part);
+    else
+      hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full,
+                         p.n_split, part);
     WAM_LAUNCHED("attention_kernel");
     const int64_t rows = (int64_t)p.n_tail * kAttnSplitQT;
     hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, *a,
@@ -504,7 +856,9 @@ int attention(const wam_attention_args* a, hipStream_t s) {
     WAM_LAUNCHED("attention_combine_kernel");
     return WAM_OK;
   }
-  if (grid8 >= 256) {
+  if (own_only && grid8 >= 128) {
+    hipLaunchKernelGGL(attention_sp_kernel, dim3((unsigned)grid8), dim3(512), 0, s, *a, (int)grid8, 1, nullptr);
+  } else if (grid8 >= 256) {
     hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1,
                        nullptr);
   } else {
