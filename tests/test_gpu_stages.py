@@ -194,7 +194,12 @@ def test_attention_strided_and_broadcast(dev):
                                                         (2, 64, 500, 321, 2, False),
                                                         (4, 33, 400, 250, 2, True),
                                                         (4, 1560, 7800, 6240, 1, True),
-                                                        (2, 1560, 7800, 5000, 2, False)])
+                                                        (2, 1560, 7800, 5000, 2, False),
+                                                        # pipelined kernel: a key block that mixes
+                                                        # pool and own keys (n_hist % 4 != 0), a
+                                                        # history shorter than one key tile
+                                                        (2, 1000, 3000, 1237, 2, False),
+                                                        (1, 3000, 100, 3, 1, True)])
 def test_attention_history(dev, B, Mq, P, nvalid, Bp, candidate):
     from wam_ops import ops
     H = 2 if Mq < 1000 else 24

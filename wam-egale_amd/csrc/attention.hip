@@ -374,8 +374,9 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 // loads straight to LDS (rows past Mk read zeros) and Q through buffer loads
 // into registers.  Lane layouts of S^T, P and O^T are those of
 // attention_kernel.
-__global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args a, int n_full, int n_split,
-                                                              float* __restrict__ part) {
+template <bool HIST>
+__global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
+                                                              int n_full, int n_split, float* __restrict__ part) {
   __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -399,12 +400,22 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
   const int b = bh % a.B, h = bh / a.B;
   const int krow = __builtin_amdgcn_readfirstlane(a.kv_rows ? clamp_row((int)a.kv_rows[b], a.kv_batch)
                                                             : clamp_row(b, a.kv_batch));
-  const int nkt = (a.Mk + kAttnKT - 1) / kAttnKT;
+  // Keys: n_hist pool rows (through the slot list) and then the Mk own keys.
+  const int n_hist = HIST ? __builtin_amdgcn_readfirstlane(*a.n_hist_dev) : 0;
+  const int n_keys = n_hist + a.Mk;
+  const int nkt = (n_keys + kAttnKT - 1) / kAttnKT;
   const int t_first = (int)((int64_t)split * nkt / ns);
   const int ntiles = (int)((int64_t)(split + 1) * nkt / ns) - t_first;
 
   const bf16* kbase = static_cast<const bf16*>(a.k) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
   const bf16* vbase = static_cast<const bf16*>(a.v) + (int64_t)krow * a.kv_bstride + h * kAttnHD;
+  const bf16 *pkbase = nullptr, *pvbase = nullptr;
+  if (HIST) {
+    const int prow = __builtin_amdgcn_readfirstlane(a.pool_rows ? clamp_row((int)a.pool_rows[b], a.pool_batch)
+                                                                : clamp_row(b, a.pool_batch));
+    pkbase = static_cast<const bf16*>(a.pool_k) + (int64_t)prow * a.pool_bstride + h * kAttnHD;
+    pvbase = static_cast<const bf16*>(a.pool_v) + (int64_t)prow * a.pool_bstride + h * kAttnHD;
+  }
   const uint32_t kv_bytes = (uint32_t)(((int64_t)(a.Mk - 1) * a.kv_rstride + kAttnHD) * 2);
   const i32x4 rk = make_rsrc4(kbase, kv_bytes), rv = make_rsrc4(vbase, kv_bytes);
   const bf16* qbase = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride + h * kAttnHD;
@@ -422,19 +433,51 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
   // Direct-to-LDS loads of a tile: wave w fills K and V blocks w and w + 8 (4
   // keys each); lane L takes key row 4g + L/16 of the tile, physical chunk
   // L % 16, and fetches the logical chunk the swizzle puts there.  For both
-  // blocks (row & 15) = 4 (w & 3) + L/16 and (row & 3) = L/16.  Keys past Mk
-  // read key Mk - 1 (finite values; their probabilities are zero).  Byte
-  // offsets are 32-bit: the host only picks this kernel when they fit.
+  // blocks (row & 15) = 4 (w & 3) + L/16 and (row & 3) = L/16.  Keys past
+  // the end read own key Mk - 1 (finite values; their probabilities are
+  // zero).  Own keys go through buffer loads with 32-bit byte offsets (the
+  // host only picks this kernel when they fit); a block that holds pool keys
+  // uses 64-bit per-lane addresses, with the 4 slots of its rows read by
+  // wave-uniform loads one step ahead (TileSlots).
   const int lr = lane >> 4, pch = lane & 15;
   const int lck = (pch ^ (4 * (wave & 3) + lr)) << 4, lcv = (pch ^ (lr << 2)) << 4;
-  auto issue = [&](int T, int st_bytes) {
+  struct TileSlots {
+    int v[2][4];
+  };
+  auto tile_slots = [&](int T) {
+    TileSlots ts{};
+    if (HIST) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int j0 = T * kAttnKT + 4 * (wave + 8 * i);
+        if (j0 < n_hist) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ts.v[i][r] = slots[min(j0 + r, n_hist - 1)];
+        }
+      }
+    }
+    return ts;
+  };
+  auto issue = [&](int T, int st_bytes, const TileSlots& ts) {
     char* sb = lds + st_bytes;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int g = wave + 8 * i;
-      const int row = min(T * kAttnKT + 4 * g + lr, a.Mk - 1) * (int)a.kv_rstride * 2;
-      asm_ld16_lds(rk, sb + g * 1024, row + lck);
-      asm_ld16_lds(rv, sb + kAttnTile + g * 1024, row + lcv);
+      const int j0 = T * kAttnKT + 4 * g;
+      if (!HIST || j0 >= n_hist) {
+        const int row = min(j0 + lr - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2;
+        asm_ld16_lds(rk, sb + g * 1024, row + lck);
+        asm_ld16_lds(rv, sb + kAttnTile + g * 1024, row + lcv);
+      } else {
+        const int j = j0 + lr;
+        const int slot = lr == 0 ? ts.v[i][0] : lr == 1 ? ts.v[i][1] : lr == 2 ? ts.v[i][2] : ts.v[i][3];
+        const int64_t own = (int64_t)min(j - n_hist, a.Mk - 1) * a.kv_rstride;
+        const int64_t pool = (int64_t)slot * a.pool_rstride;
+        const char* ks = reinterpret_cast<const char*>(j < n_hist ? pkbase + pool : kbase + own);
+        const char* vs = reinterpret_cast<const char*>(j < n_hist ? pvbase + pool : vbase + own);
+        asm_g_ld16_lds((uint64_t)(uintptr_t)(ks + lck), sb + g * 1024);
+        asm_g_ld16_lds((uint64_t)(uintptr_t)(vs + lcv), sb + kAttnTile + g * 1024);
+      }
     }
   };
   constexpr int kVmTile = 4;  // direct-to-LDS loads per wave per tile
@@ -540,7 +583,7 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
   // any lane; alpha is the factor O must then be scaled by (1 elsewhere).
   auto softmax = [&](f32x16 (&s)[2], int T, auto mask_tag, float& alpha) -> bool {
     if constexpr (decltype(mask_tag)::value) {
-      const int valid = a.Mk - T * kAttnKT;
+      const int valid = n_keys - T * kAttnKT;
       // key kt*32 + 8 (v / 4) + 4 half + v % 4 is past the end: compare the
       // compile-time part against one per-lane threshold
       const int thr = valid - 4 * half;
@@ -612,8 +655,8 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
   if (ntiles > 0) {
     // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
     // tile 0 has landed.
-    issue(t_first, 0);
-    if (ntiles > 1) issue(t_first + 1, kAttnStage);
+    issue(t_first, 0, tile_slots(t_first));
+    if (ntiles > 1) issue(t_first + 1, kAttnStage, tile_slots(t_first + 1));
     if (ntiles > 1) __builtin_amdgcn_s_waitcnt((kVmTile & 15) | (7 << 4) | (15 << 8));
     else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __builtin_amdgcn_s_barrier();
@@ -627,10 +670,12 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
     auto step = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
       const int T = t_first + t;
       const bool has_next = t + 1 < ntiles;
+      // pool slots of tile t+2, read while the wait below runs
+      const TileSlots ts = tile_slots(T + 2);
       // tile t+1 has landed and every wave is done with the stage of t-1
       if (has_next) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
       __builtin_amdgcn_s_barrier();
-      if (t + 2 < ntiles) issue(T + 2, st2);
+      if (t + 2 < ntiles) issue(T + 2, st2, ts);
       float alpha;
       s_mfma(has_next ? st1 : st0, snxt);
       const bool moved = softmax(scur, T, mask_tag, alpha);
@@ -652,7 +697,7 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
     };
     const std::integral_constant<bool, false> full;
     const std::integral_constant<bool, true> last;
-    const int nm = ntiles - 1;  // tiles before the last one hold no key past Mk
+    const int nm = ntiles - 1;  // tiles before the last one hold no key past the end
     int t = 0;
     for (; t + 1 < nm; t += 2) {
       step(t, s0, s1, full);
@@ -799,8 +844,8 @@ int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
   return plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX));
 }
 
-// Selects the software-pipelined kernel for calls without a KV pool (a switch for
-// side-by-side measurement; always on in the library).
+// Selects the software-pipelined kernel (a switch for side-by-side
+// measurement; always on in the library).
 static bool g_attn_w4 = true;
 
 int attention(const wam_attention_args* a, hipStream_t s) {
@@ -835,16 +880,16 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   WAM_REQUIRE(grid8 < (1 << 26), "wam_attention: grid too large");
   const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
   const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0);
-  // Keys of this call only (no KV pool), with every Q and K/V row's byte
-  // offset inside 31 bits: the software-pipelined kernel.
-  const bool own_only = a->n_hist_dev == nullptr && g_attn_w4 &&
-                        ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
-                        ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
+  // The software-pipelined kernel when every Q and own K/V row's byte
+  // offset fits in 31 bits (pool rows use 64-bit addresses).
+  const bool sp = g_attn_w4 && ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
+                  ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
+  auto sp_kernel = a->n_hist_dev ? attention_sp_kernel<true> : attention_sp_kernel<false>;
   if (p.n_split > 1) {
     float* part = static_cast<float*>(a->workspace);
     const int64_t grid = (int64_t)p.n_full + (int64_t)p.n_tail * p.n_split;
-    if (own_only)
-      hipLaunchKernelGGL(attention_sp_kernel, dim3((unsigned)grid), dim3(512), 0, s, *a, p.n_full, p.n_split,
+    if (sp)
+      hipLaunchKernelGGL(sp_kernel, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full, p.n_split,
                          part);
     else
       hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full,
@@ -856,8 +901,8 @@ int attention(const wam_attention_args* a, hipStream_t s) {
     WAM_LAUNCHED("attention_combine_kernel");
     return WAM_OK;
   }
-  if (own_only && grid8 >= 128) {
-    hipLaunchKernelGGL(attention_sp_kernel, dim3((unsigned)grid8), dim3(512), 0, s, *a, (int)grid8, 1, nullptr);
+  if (sp && grid8 >= 128) {
+    hipLaunchKernelGGL(sp_kernel, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1, nullptr);
   } else if (grid8 >= 256) {
     hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1,
                        nullptr);
