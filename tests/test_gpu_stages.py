@@ -33,7 +33,9 @@ def _ref_linear(x, w, b):
 
 @pytest.mark.parametrize("M,K,N,nseg", [(1, 64, 128, 1), (300, 256, 384, 1), (77, 512, 256, 3),
                                         (4680, 3072, 3072, 1), (520, 3072, 3072, 3),
-                                        (300, 256, 192, 1), (70, 192, 200, 1), (4680, 3072, 192, 1)])
+                                        (300, 256, 192, 1), (70, 192, 200, 1), (4680, 3072, 192, 1),
+                                        # 224-row tiles: 21 x 36 tiles over three segments
+                                        (4680, 3072, 3072, 3)])
 def test_linear_bias(dev, M, K, N, nseg):
     from wam_ops import ops
     x = _randn((M, K), dev, 1)
@@ -56,10 +58,14 @@ def test_linear_bias(dev, M, K, N, nseg):
 # with the epilogue); (3900, 4160, 4352) does so with a partial last row tile
 # and 65 k-tiles in 8 uneven ranges.  (300, 512, 200) ends in a partial
 # column tile (72 of 128 columns), so lanes past N skip the residual loads
-# issued ahead of the LDS staging as well as the stores.
+# issued ahead of the LDS staging as well as the stores.  (4680, 3072, 3072),
+# (4680, 14336, 3072) and (4500, 4160, 3072) run on 224-row tiles (21 row
+# tiles; the last one of 4500 holds 20 rows, over 65 k-tiles), every
+# epilogue included.
 @pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
                                    (4680, 256, 14336), (6240, 3072, 2816), (6240, 6144, 3072),
-                                   (3900, 4160, 4352), (300, 512, 200)])
+                                   (3900, 4160, 4352), (300, 512, 200), (4680, 3072, 3072),
+                                   (4680, 14336, 3072), (4500, 4160, 3072)])
 def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     D = N

@@ -514,30 +514,46 @@ struct CfgW4 {
   static constexpr int BM = 256, BN = 256, BK = 64, WB = 2, kThreads = 256;
   static constexpr bool kW4 = true;
 };
+// The same kernel on 224 x 256 tiles, the four waves side by side along n
+// (224 x 64 each, 7 x 2 MFMA blocks): 4680 rows are 21 such tiles (0.5% of
+// padding against 3.9% for 19 x 256), and a 3072-column GEMM then fills 252
+// of the 256 CUs in one round of 7/8 of a 256-row tile's work.
+struct CfgW4t224 {
+  static constexpr int BM = 224, BN = 256, BK = 64, WB = 2, kThreads = 256;
+  static constexpr bool kW4 = true;
+};
 
-// The 16 MFMAs of one 16-deep sub-step with the 8 fragment reads of the next
-// sub-step (one after every second MFMA), W LDS writes and V global loads
-// spread evenly between them.
-template <int W, int V>
+// The NM MFMAs of one 16-deep sub-step with the NR fragment reads of the
+// next sub-step, W LDS writes and V global loads spread evenly between them
+// (NM = 16, NR = 8: one read after every second MFMA).
+template <int W, int V, int NM, int NR>
 __device__ __forceinline__ void w4_sched() {
 #pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                   // MFMA
-    if (q & 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // DS read
-    if ((q * W) / 16 != ((q + 1) * W) / 16) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-    if ((q * V) / 16 != ((q + 1) * V) / 16) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+  for (int q = 0; q < NM; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     // MFMA
+    if ((q * NR) / NM != ((q + 1) * NR) / NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    if ((q * W) / NM != ((q + 1) * W) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);    // DS write
+    if ((q * V) / NM != ((q + 1) * V) / NM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read
   }
 }
 
 // RF32 / OF32: the residual / output is fp32 (else bf16); compile-time so
-// that the epilogue's loads and stores are branch-free.
-template <int EPI, int RF32, int OF32>
+// that the epilogue's loads and stores are branch-free.  TM: tile rows, 256
+// (waves 2 x 2, 128 x 128 each) or 224 (waves 1 x 4, 224 x 64 each).
+template <int EPI, int RF32, int OF32, int TM>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
+  static_assert(TM == 256 || TM == 224, "tile rows");
+  constexpr int MB = TM == 256 ? 4 : 7;   // 32-row m-blocks per wave
+  constexpr int NB = TM == 256 ? 4 : 2;   // 32-column n-blocks per wave
+  constexpr int WGN = TM == 256 ? 2 : 4;  // waves along n
+  constexpr int LA = TM / 32;             // A staging loads per thread and k-step
+  constexpr int NL = LA + 8;              // and the 8 of W
+  constexpr int NM = MB * NB, NR = MB + NB;  // MFMAs and fragment reads per sub-step
   __shared__ __attribute__((aligned(1024))) char L0[65536];
   __shared__ __attribute__((aligned(1024))) char L1[65536];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int half = lane >> 5, l32 = lane & 31;
 
   // Tile order: XCD-contiguous ranges, then groups of 8 m-tiles swept along n.
@@ -557,7 +573,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   const int tn = __builtin_amdgcn_readfirstlane(in_group / gsize);
   const int seg = __builtin_amdgcn_readfirstlane(tn / p.n_tiles_per_seg);
   const int n0 = (tn - seg * p.n_tiles_per_seg) * 256;
-  const int m0 = tm * 256;
+  const int m0 = tm * TM;
 
   int nk = p.K / 64, kb = 0;
   if constexpr (EPI == kEpiPartial) {
@@ -574,57 +590,59 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   auto res_a = [&](int kt) { return make_rsrc(abase + kt * 128, abytes - (uint32_t)kt * 128u); };
   auto res_b = [&](int kt) { return make_rsrc(bbase + kt * 128, bbytes - (uint32_t)kt * 128u); };
 
-  // Staging: load i (0..15) of a thread is row 32 (i & 7) + tid / 8 of A
-  // (i < 8) or W (i >= 8), 16-byte chunk tid % 8.  Its LDS slot is that row's
-  // chunk under the swizzle; (row >> 1) & 7 does not depend on i.
+  // Staging: load i (0..NL-1) of a thread is row 32 i + tid / 8 of A (i < LA)
+  // or row 32 (i - LA) + tid / 8 of W, 16-byte chunk tid % 8.  Its LDS slot
+  // is that row's chunk under the swizzle; (row >> 1) & 7 does not depend on i.
   const int lr = tid >> 3, lc = tid & 7;
   const int va = lr * (int)p.lda * 2 + lc * 16, vb = lr * (int)p.ldw * 2 + lc * 16;
   const int ra32 = 32 * (int)p.lda * 2, rb32 = 32 * (int)p.ldw * 2;
   const int wofs = lds_off<8>(lr, lc);
   typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
-  u32x4s S0[16], S1[16];
+  u32x4s S0[NL], S1[NL];
   auto gload = [&](u32x4s* S, int kt, auto lo_c, auto hi_c) {
     constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
     const __amdgpu_buffer_rsrc_t ra = res_a(kt), rb = res_b(kt);
 #pragma unroll
     for (int i = LO; i < HI; ++i) {
-      if (i < 8) S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(ra, va + i * ra32, 0, 0));
-      else S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(rb, vb + (i - 8) * rb32, 0, 0));
+      if (i < LA) S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(ra, va + i * ra32, 0, 0));
+      else S[i] = __builtin_bit_cast(u32x4s, __builtin_amdgcn_raw_buffer_load_b128(rb, vb + (i - LA) * rb32, 0, 0));
     }
   };
   auto swrite = [&](u32x4s* S, char* buf, auto lo_c, auto hi_c) {
     constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
 #pragma unroll
     for (int i = LO; i < HI; ++i)
-      *reinterpret_cast<u32x4s*>(buf + (i >= 8 ? 32768 : 0) + (i & 7) * 4096 + wofs) = S[i];
+      *reinterpret_cast<u32x4s*>(buf + (i >= LA ? 32768 + (i - LA) * 4096 : i * 4096) + wofs) = S[i];
   };
+  // The staging sets go to LDS and are reloaded in three parts over a k-step.
+  constexpr int P1 = NL == 16 ? 6 : 5, P2 = NL == 16 ? 11 : 10;
   using I0 = std::integral_constant<int, 0>;
-  using I5 = std::integral_constant<int, 5>;
-  using I6 = std::integral_constant<int, 6>;
-  using I11 = std::integral_constant<int, 11>;
-  using I16 = std::integral_constant<int, 16>;
+  using IP1 = std::integral_constant<int, P1>;
+  using IP2 = std::integral_constant<int, P2>;
+  using INL = std::integral_constant<int, NL>;
 
-  f32x16 acc[4][4];
+  f32x16 acc[NB][MB];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < NB; ++j)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[j][i] = f32x16{};
-  // Fragments of a sub-step: rows wm*128 + 32 i + l32 of A and wn*128 + 32 j
-  // + l32 of W at logical chunk 2 s + half; the swizzle term is (l32 >> 1) & 7.
-  bf16x8 fa[2][4], fb[2][4];
-  const int rowa = (wm * 128 + l32) * 128, rowb = 32768 + (wn * 128 + l32) * 128;
+    for (int i = 0; i < MB; ++i) acc[j][i] = f32x16{};
+  // Fragments of a sub-step: rows wm*32*MB + 32 i + l32 of A and wn*32*NB +
+  // 32 j + l32 of W at logical chunk 2 s + half; the swizzle term is
+  // (l32 >> 1) & 7.
+  bf16x8 fa[2][MB], fb[2][NB];
+  const int rowa = (wm * 32 * MB + l32) * 128, rowb = 32768 + (wn * 32 * NB + l32) * 128;
   auto rd = [&](const char* buf, int s, int f) {
     const int xo = ((2 * s + half) ^ ((l32 >> 1) & 7)) << 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[f][i] = ld_bf16x8(buf + rowa + i * 4096 + xo);
+    for (int i = 0; i < MB; ++i) fa[f][i] = ld_bf16x8(buf + rowa + i * 4096 + xo);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fb[f][j] = ld_bf16x8(buf + rowb + j * 4096 + xo);
+    for (int j = 0; j < NB; ++j) fb[f][j] = ld_bf16x8(buf + rowb + j * 4096 + xo);
   };
   auto mm = [&](int f) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MB; ++i)
         acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[f][j], fa[f][i], acc[j][i], 0, 0, 0);
   };
 
@@ -632,10 +650,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   // k-tile 2 into set 0.  Loads past the last k-tile repeat it: unconditional
   // register writes keep the staging sets out of control-flow merges, which
   // made the register allocator copy and spill them.
-  gload(S0, 0, I0{}, I16{});
-  gload(S1, min(1, nk - 1), I0{}, I16{});
-  swrite(S0, L0, I0{}, I16{});
-  gload(S0, min(2, nk - 1), I0{}, I16{});
+  gload(S0, 0, I0{}, INL{});
+  gload(S1, min(1, nk - 1), I0{}, INL{});
+  swrite(S0, L0, I0{}, INL{});
+  gload(S0, min(2, nk - 1), I0{}, INL{});
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
   rd(L0, 0, 0);
@@ -645,30 +663,30 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   auto kstep = [&](int t, char* cur, char* nxt, u32x4s* Snext) {
     const int kt3 = min(t + 3, nk - 1);
     rd(cur, 1, 1);
-    swrite(Snext, nxt, I0{}, I6{});
+    swrite(Snext, nxt, I0{}, IP1{});
     mm(0);
-    w4_sched<6, 0>();
+    w4_sched<P1, 0, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     rd(cur, 2, 0);
-    swrite(Snext, nxt, I6{}, I11{});
-    gload(Snext, kt3, I0{}, I6{});
+    swrite(Snext, nxt, IP1{}, IP2{});
+    gload(Snext, kt3, I0{}, IP1{});
     mm(1);
-    w4_sched<5, 6>();
+    w4_sched<P2 - P1, P1, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     rd(cur, 3, 1);
-    swrite(Snext, nxt, I11{}, I16{});
-    gload(Snext, kt3, I6{}, I11{});
+    swrite(Snext, nxt, IP2{}, INL{});
+    gload(Snext, kt3, IP1{}, IP2{});
     mm(0);
-    w4_sched<5, 5>();
+    w4_sched<NL - P2, P2 - P1, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     // Every wave has written its part of the next stage and read its last
     // fragments of this one.
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
     rd(nxt, 0, 0);
-    gload(Snext, kt3, I11{}, I16{});
+    gload(Snext, kt3, IP2{}, INL{});
     mm(1);
-    w4_sched<0, 5>();
+    w4_sched<0, NL - P2, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
   };
   // Pairs of k-steps without a condition inside (a conditional second step
@@ -704,7 +722,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   float gate[4] = {0.f, 0.f, 0.f, 0.f};
   bool gate_once = false;
   if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + 256, p.M) - 1);
+    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + TM, p.M) - 1);
     if (gate_once) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
   }
   constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
@@ -734,17 +752,22 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   const int ld_out = PART ? p.seg_n : (int)p.ldo;
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
   typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
-  // tile row handled by pass ps (0..31) of round r
+  // Tile row handled by pass ps (0..31) of round r: rows 64 r .. +64 of each
+  // wave row (TM = 256), or rows 128 r .. +128 (TM = 224, whose second round
+  // has 96 rows, passes 0..23).
   auto row_of = [&](int r, int ps) {
     const int rr = ps * 4 + (tid >> 6);
-    return (rr >> 6) * 128 + 64 * r + (rr & 63);
+    return TM == 256 ? (rr >> 6) * 128 + 64 * r + (rr & 63) : 128 * r + rr;
   };
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
+  // One round; r is a compile-time constant, so the pass loops below unroll
+  // and the residual registers are never indexed at run time.
+  auto round = [&](auto r_c) {
+    constexpr int r = decltype(r_c)::value;
+    constexpr int nps = (TM == 224 && r == 1) ? 24 : 32;
     u32x4v rraw[RES ? 32 : 1];
     if constexpr (RES) {
 #pragma unroll
-      for (int ps = 0; ps < 32; ++ps) {
+      for (int ps = 0; ps < nps; ++ps) {
         const int off = (row_of(r, ps) * (int)p.ldr + 4 * q) * RB;
         if constexpr (RF32) {
           rraw[ps] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0));
@@ -756,17 +779,20 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
-    {
-      char* buf = wm ? L1 : L0;
+    // The wave's m-blocks of this round, as 1 KB fp32 rows: TM = 256, blocks
+    // 2r and 2r+1 into L0 (wave row 0) or L1 (wave row 1); TM = 224, blocks
+    // 4r .. 4r+3 (of 7), two into each buffer.
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
+    for (int ii = 0; ii < (TM == 256 ? 2 : 4); ++ii) {
+      const int i = TM == 256 ? 2 * r + ii : 4 * r + ii;
+      if (i >= MB) continue;
+      char* buf = (TM == 256 ? wm : ii >> 1) ? L1 : L0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int i = 2 * r + ii;
-            const int lrw = ii * 32 + l32;
-            const int qq = wn * 32 + j * 8 + 2 * g + half;
+            const int lrw = (ii & 1) * 32 + l32;
+            const int qq = wn * 8 * NB + j * 8 + 2 * g + half;
             f32x4 v;
             if (g == 0) v = __builtin_shufflevector(acc[j][i], acc[j][i], 0, 1, 2, 3);
             else if (g == 1) v = __builtin_shufflevector(acc[j][i], acc[j][i], 4, 5, 6, 7);
@@ -778,7 +804,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int b8 = 0; b8 < 4; ++b8) {
+    for (int b8 = 0; b8 < nps / 8; ++b8) {
       f32x4 vv[8];
 #pragma unroll
       for (int k8 = 0; k8 < 8; ++k8) {
@@ -845,7 +871,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
       // one batch of LDS reads live at a time
       __builtin_amdgcn_sched_barrier(0);
     }
-  }
+  };
+  round(std::integral_constant<int, 0>{});
+  round(std::integral_constant<int, 1>{});
 }
 
 // Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
@@ -902,12 +930,16 @@ static void launch_tiles(dim3 grid, const LinearParams& p, hipStream_t s) {
   if constexpr (C::kW4) {
     constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
     if constexpr (RES) {
-      if (p.res_f32 && p.out_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 1>), grid, dim3(C::kThreads), 0, s, p);
-      else if (p.res_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 0>), grid, dim3(C::kThreads), 0, s, p);
-      else if (p.out_f32) hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 1>), grid, dim3(C::kThreads), 0, s, p);
-      else hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0>), grid, dim3(C::kThreads), 0, s, p);
+      if (p.res_f32 && p.out_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 1, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+      else if (p.res_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+      else if (p.out_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 1, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
     } else {
-      hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0>), grid, dim3(C::kThreads), 0, s, p);
+      hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
     }
   } else {
     hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI>), grid, dim3(C::kThreads), 0, s, p);
@@ -1041,6 +1073,22 @@ static int launch_big(LinearParams& p, int64_t ws_bytes, hipStream_t s) {
   return launch_gemm<CBig>(tail, s);
 }
 
+// Cost of a launch in 256x256-tile times: the 256-row plan (whole rounds,
+// or rounds plus a tail, gemm_plan) against one launch of 224-row tiles,
+// whose rounds take 7/8 as long.
+static bool w4_t224_wins(int M, int seg_n, int n_seg, int K, int cus, int64_t ws_bytes) {
+  const int64_t nt = (int64_t)(seg_n / 256) * n_seg;
+  const int64_t t256 = (int64_t)((M + 255) / 256) * nt, t224 = (int64_t)((M + 223) / 224) * nt;
+  double c256 = (double)((t256 + cus - 1) / cus);
+  const GemmPlan g = gemm_plan(M, seg_n, n_seg, K, cus, ws_bytes);
+  if (g.kind != 0) {
+    // the plan's tail costs at most what it replaces; count it as a quarter round
+    c256 = (double)(t256 / cus) + 0.25;
+  }
+  const double c224 = (double)((t224 + cus - 1) / cus) * (224.0 / 256.0);
+  return c224 < c256 - 1e-9;
+}
+
 // Whether linear() takes the 256x256 path for this shape.
 static bool uses_big_tiles(int M, int seg_n, int n_seg) {
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * (seg_n / 256) * n_seg;
@@ -1112,13 +1160,18 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     return launch_gemm<Cfg128x128f8>(p, s);
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
-  // The four-wave kernel has the faster k loop; its epilogue reads residual
-  // rows with one wave per SIMD, which costs more than the loop gains when the
-  // loop is short (measured on 4680 and 6240 x 3072 x 3072 with the gated and
-  // plain residual epilogues: 4-12% slower than the eight-wave kernel; every
-  // other block GEMM 0-10% faster).
+  // The four-wave kernel has the faster k loop.  On 224-row tiles it wins
+  // whenever those need fewer tile-times (4680 rows: QKV 240 -> 226 us,
+  // 4680 x 3072 x 3072 78 -> 75 us, FFN2 335 -> 321 us, the gated-residual
+  // projection 95 -> 92 us against the eight-wave kernel).  On 256-row tiles
+  // its epilogue reads residual rows with one wave per SIMD, which costs more
+  // than the loop gains when the loop is short (4680 and 6240 x 3072 x 3072
+  // with the gated and plain residual epilogues: 4-12% slower than the
+  // eight-wave kernel; every other block GEMM 0-10% faster).
   if (big) {
     const bool res = a->epilogue == WAM_EPI_BIAS_GATE_RES || a->epilogue == WAM_EPI_BIAS_RES;
+    if (w4_t224_wins(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes))
+      return launch_gemm<CfgW4t224>(p, s);
     if (res && a->K <= 4096) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
     return launch_big<CfgW4, Cfg128x128w4>(p, ws_bytes, s);
   }
