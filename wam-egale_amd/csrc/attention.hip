@@ -20,6 +20,7 @@
 // pool rows into a contiguous tensor (pack_kernel,
 // 算子研究/wam_ops/baseline/csrc/block.cu:213-224); here the pool is read in
 // place through the slot list.
+#include <algorithm>
 #include <mutex>
 #include "wam_common.h"
 
@@ -374,14 +375,16 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 // loads straight to LDS (rows past Mk read zeros) and Q through buffer loads
 // into registers.  Lane layouts of S^T, P and O^T are those of
 // attention_kernel.
-template <bool HIST>
-__global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
-                                                              int n_full, int n_split, float* __restrict__ part) {
-  __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage];
+template <bool HIST, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
+                                                                  int n_full, int n_split, float* __restrict__ part) {
+  static_assert(NW == 7 || NW == 8, "7 or 8 waves");
+  // three K/V stages, then (pool keys only) the 64 slots of each stage's tile
+  __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage + (HIST ? 3 * kAttnKT * 4 : 0)];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, half = lane >> 5;
-  constexpr int QT = 256;
+  constexpr int QT = 32 * NW;
   const int nqt = (a.Mq + QT - 1) / QT;
   const int n_tail = nqt * a.H * a.B - n_full;
   int unit, split = 0, ns = 1;
@@ -430,57 +433,61 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
     qf[ks] = __builtin_bit_cast(
         bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rq, (qi * (int)a.q_rstride + 16 * ks + 8 * half) * 2, 0, 0));
 
-  // Direct-to-LDS loads of a tile: wave w fills K and V blocks w and w + 8 (4
-  // keys each); lane L takes key row 4g + L/16 of the tile, physical chunk
-  // L % 16, and fetches the logical chunk the swizzle puts there.  For both
-  // blocks (row & 15) = 4 (w & 3) + L/16 and (row & 3) = L/16.  Keys past
-  // the end read own key Mk - 1 (finite values; their probabilities are
-  // zero).  Own keys go through buffer loads with 32-bit byte offsets (the
-  // host only picks this kernel when they fit); a block that holds pool keys
-  // uses 64-bit per-lane addresses, with the 4 slots of its rows read by
-  // wave-uniform loads one step ahead (TileSlots).
+  // Direct-to-LDS loads of a tile: 32 one-KB sub-blocks (K blocks 0-15, then
+  // V blocks 0-15, 4 keys each); wave w takes sub-blocks w, w + NW, ... (4
+  // per wave with 8 waves; 5 for waves 0-3 and 4 for waves 4-6 with 7).
+  // Lane L takes key row 4 blk + L/16 of its block, physical chunk L % 16,
+  // and fetches the logical chunk the swizzle puts there: (row & 15) =
+  // 4 (blk & 3) + L/16 for K, (row & 3) = L/16 for V.  Keys past the end read
+  // own key Mk - 1 (finite values; their probabilities are zero).  Own keys go
+  // through buffer loads with 32-bit byte offsets (the host only picks this
+  // kernel when they fit); a block that holds pool keys uses 64-bit per-lane
+  // addresses, with the slots of its rows read from the stage's slot list in
+  // LDS (load_slots, one step ahead).
+  constexpr int kSub = (32 + NW - 1) / NW;  // sub-block slots per wave
+  const int nsub = (32 - wave + NW - 1) / NW;
   const int lr = lane >> 4, pch = lane & 15;
-  const int lck = (pch ^ (4 * (wave & 3) + lr)) << 4, lcv = (pch ^ (lr << 2)) << 4;
-  struct TileSlots {
-    int v[2][4];
-  };
-  auto tile_slots = [&](int T) {
-    TileSlots ts{};
-    if (HIST) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int j0 = T * kAttnKT + 4 * (wave + 8 * i);
-        if (j0 < n_hist) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) ts.v[i][r] = slots[min(j0 + r, n_hist - 1)];
-        }
-      }
+  // Slot list of the tile bound for stage st_bytes (64 ints).
+  auto slot_list = [&](int st_bytes) { return lds + 3 * kAttnStage + (st_bytes >> 15) * (kAttnKT * 4); };
+  static_assert(kAttnStage == 1 << 15, "stage index is st_bytes >> 15");
+  // The last wave (one of those with the fewest sub-blocks) copies the 64
+  // slots of tile T into the list of its stage: lane L slot T*64 + L.
+  auto load_slots = [&](int T, int st_bytes) {
+    if (HIST && wave == NW - 1 && T * kAttnKT < n_hist) {
+      const int* src = slots + min(T * kAttnKT + lane, n_hist - 1);
+      asm_g_ld4_lds((uint64_t)(uintptr_t)src, slot_list(st_bytes));
     }
-    return ts;
   };
-  auto issue = [&](int T, int st_bytes, const TileSlots& ts) {
+  auto issue = [&](int T, int st_bytes) {
     char* sb = lds + st_bytes;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int g = wave + 8 * i;
-      const int j0 = T * kAttnKT + 4 * g;
+    for (int i = 0; i < kSub; ++i) {
+      const int sbk = wave + NW * i;
+      if (sbk >= 32) break;
+      const bool isk = sbk < 16;
+      const int blk = sbk & 15;
+      const int j0 = T * kAttnKT + 4 * blk;
+      const int lc = (isk ? (pch ^ (4 * (blk & 3) + lr)) : (pch ^ (lr << 2))) << 4;
+      char* dst = sb + (isk ? 0 : kAttnTile) + blk * 1024;
       if (!HIST || j0 >= n_hist) {
         const int row = min(j0 + lr - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2;
-        asm_ld16_lds(rk, sb + g * 1024, row + lck);
-        asm_ld16_lds(rv, sb + kAttnTile + g * 1024, row + lcv);
+        asm_ld16_lds(isk ? rk : rv, dst, row + lc);
       } else {
         const int j = j0 + lr;
-        const int slot = lr == 0 ? ts.v[i][0] : lr == 1 ? ts.v[i][1] : lr == 2 ? ts.v[i][2] : ts.v[i][3];
-        const int64_t own = (int64_t)min(j - n_hist, a.Mk - 1) * a.kv_rstride;
-        const int64_t pool = (int64_t)slot * a.pool_rstride;
-        const char* ks = reinterpret_cast<const char*>(j < n_hist ? pkbase + pool : kbase + own);
-        const char* vs = reinterpret_cast<const char*>(j < n_hist ? pvbase + pool : vbase + own);
-        asm_g_ld16_lds((uint64_t)(uintptr_t)(ks + lck), sb + g * 1024);
-        asm_g_ld16_lds((uint64_t)(uintptr_t)(vs + lcv), sb + kAttnTile + g * 1024);
+        const int slot = *reinterpret_cast<const int*>(slot_list(st_bytes) + (4 * blk + lr) * 4);
+        const bf16* pb0 = isk ? pkbase : pvbase;
+        const bf16* ob0 = isk ? kbase : vbase;
+        const char* src = reinterpret_cast<const char*>(
+            j < n_hist ? pb0 + (int64_t)slot * a.pool_rstride : ob0 + (int64_t)min(j - n_hist, a.Mk - 1) * a.kv_rstride);
+        asm_g_ld16_lds((uint64_t)(uintptr_t)(src + lc), dst);
       }
     }
   };
-  constexpr int kVmTile = 4;  // direct-to-LDS loads per wave per tile
+  // Wait until at most one tile's loads of this wave are in flight.
+  auto wait_all_but_one_tile = [&]() {
+    if (NW == 8 || nsub == 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8));
+    else __builtin_amdgcn_s_waitcnt(5 | (7 << 4) | (15 << 8));
+  };
 
   const float sc = a.scale * kLog2e;
   const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
@@ -655,9 +662,18 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
   if (ntiles > 0) {
     // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
     // tile 0 has landed.
-    issue(t_first, 0, tile_slots(t_first));
-    if (ntiles > 1) issue(t_first + 1, kAttnStage, tile_slots(t_first + 1));
-    if (ntiles > 1) __builtin_amdgcn_s_waitcnt((kVmTile & 15) | (7 << 4) | (15 << 8));
+    if (HIST) {
+      // slot lists of the first three tiles, visible to every wave
+      load_slots(t_first, 0);
+      if (ntiles > 1) load_slots(t_first + 1, kAttnStage);
+      if (ntiles > 2) load_slots(t_first + 2, 2 * kAttnStage);
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    issue(t_first, 0);
+    if (ntiles > 1) issue(t_first + 1, kAttnStage);
+    if (ntiles > 1) wait_all_but_one_tile();
     else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __builtin_amdgcn_s_barrier();
     s_mfma(0, s0);
@@ -670,12 +686,14 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
     auto step = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
       const int T = t_first + t;
       const bool has_next = t + 1 < ntiles;
-      // pool slots of tile t+2, read while the wait below runs
-      const TileSlots ts = tile_slots(T + 2);
-      // tile t+1 has landed and every wave is done with the stage of t-1
+      // tile t+1 (and the slot list of t+2) has landed and every wave is
+      // done with the stage of t-1 (and with the slot list of t, read two
+      // steps ago)
       if (has_next) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
       __builtin_amdgcn_s_barrier();
-      if (t + 2 < ntiles) issue(T + 2, st2, ts);
+      if (HIST) asm volatile("" ::: "memory");  // slot reads stay below the barrier
+      if (t + 2 < ntiles) issue(T + 2, st2);
+      if (t + 3 < ntiles) load_slots(T + 3, st0);
       float alpha;
       s_mfma(has_next ? st1 : st0, snxt);
       const bool moved = softmax(scur, T, mask_tag, alpha);
@@ -748,11 +766,10 @@ __global__ __launch_bounds__(512, 1) void attention_sp_kernel(wam_attention_args
 // O = sum_i 2^(m_i - m) O_i / sum_i 2^(m_i - m) l_i with m = max_i m_i.  One
 // wave per (split unit, query) row, two of the 128 outputs per lane; every
 // range's loads are issued before any of them is used.
-constexpr int kAttnSplitQT = 256;  // the split path runs the 8-wave kernel
+// QT: query rows per unit (256, or 224 for the 7-wave pipelined kernel).
 constexpr int kAttnMaxSplit = 8;
 __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_args a, int n_full, int n_split,
-                                                                const float* __restrict__ part) {
-  constexpr int QT = kAttnSplitQT;
+                                                                int QT, const float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
   const int nqt = (a.Mq + QT - 1) / QT;
   const int n_tail = nqt * a.H * a.B - n_full;
@@ -794,10 +811,10 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
   *reinterpret_cast<bf16x2*>(op + 2 * lane) = r;
 }
 
-// Launch plan of the split path: the first n_full units run whole, the other
-// n_tail units are split into n_split key ranges each.  Cost model, in units
-// of one whole unit's run time on one CU (kt key tiles of 64 keys), for C
-// CUs (256 on MI355X) taking workgroups in dispatch order:
+// Launch plan of the split path: the first n_full units (of QT query rows)
+// run whole, the other n_tail units are split into n_split key ranges each.
+// Cost model, in units of one whole unit's run time on one CU (kt key tiles of
+// 64 keys), for C CUs (256 on MI355X) taking workgroups in dispatch order:
 //   n_full / C  +  ceil(pieces / C) * (1 / n_split + kFill / kt)
 //                 +  pieces * kCombine / kt,         pieces = n_tail * n_split
 // kFill: key tiles' worth of pipeline fill and partial-result store per
@@ -807,46 +824,70 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
 // none beats the whole-unit grid.  E.g. 4 x 1560 queries over 7800 keys (672
 // units, kt 122): 512 whole + 160 units in 3 ranges, 2.74 vs 3 rounds.
 struct AttnPlan {
-  int n_full, n_split, n_tail;
+  int n_full, n_split, n_tail, qt;
+  double cost;  // in whole-unit times of this plan's units
 };
-constexpr int64_t kPartBytesPerPiece = (int64_t)kAttnSplitQT * (kAttnHD + 2) * 4;
 
 static int64_t plan_bytes(const AttnPlan& p) {
-  return p.n_split > 1 ? (int64_t)p.n_split * p.n_tail * kPartBytesPerPiece : 0;
+  return p.n_split > 1 ? (int64_t)p.n_split * p.n_tail * p.qt * (kAttnHD + 2) * 4 : 0;
 }
 
-static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_bytes) {
+static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_bytes, int QT) {
   const int cus = device_cu_count();
   constexpr double kFill = 1.5, kCombine = 0.0133;
-  const int64_t units = (int64_t)((Mq + kAttnSplitQT - 1) / kAttnSplitQT) * H * B;
-  AttnPlan best{(int)units, 1, 0};
+  const int64_t units = (int64_t)((Mq + QT - 1) / QT) * H * B;
+  const int64_t piece_bytes = (int64_t)QT * (kAttnHD + 2) * 4;
+  AttnPlan best{(int)units, 1, 0, QT, (double)((units + cus - 1) / cus)};
   if (units <= 0 || units >= (1 << 26)) return best;
   const double kt = (double)((keys > 0 ? keys : 1) + kAttnKT - 1) / kAttnKT;
-  double best_cost = (double)((units + cus - 1) / cus);
   for (int64_t F = 0; F < units; F += cus) {
     const int64_t T = units - F;
     for (int ns = 2; ns <= kAttnMaxSplit; ++ns) {
       const int64_t pieces = T * ns;
-      if (pieces * kPartBytesPerPiece > max_bytes) break;
+      if (pieces * piece_bytes > max_bytes) break;
       const double cost = (double)F / cus +
                           (double)((pieces + cus - 1) / cus) * (1.0 / ns + kFill / kt) +
                           (double)pieces * kCombine / kt;
-      if (cost < best_cost - 1e-9) {
-        best_cost = cost;
-        best = AttnPlan{(int)F, ns, (int)T};
-      }
+      if (cost < best.cost - 1e-9) best = AttnPlan{(int)F, ns, (int)T, QT, cost};
     }
   }
   return best;
 }
 
-int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
-  return plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX));
-}
-
 // Selects the software-pipelined kernel (a switch for side-by-side
 // measurement; always on in the library).
 static bool g_attn_w4 = true;
+
+// The pipelined kernel runs when every Q and own K/V row's byte offset fits in
+// 31 bits (pool rows use 64-bit addresses) and the query grid is at least 128
+// units of 256 rows; smaller grids use attention_kernel<4>.
+static bool sp_eligible(const wam_attention_args* a) {
+  const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
+  return g_attn_w4 && grid8 >= 128 && ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
+         ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
+}
+
+// Query rows per unit of the pipelined kernel: 224 (7 waves) when its plan,
+// in unit-times of 7/8 of a 256-row unit, costs less than the 256-row plan.
+// 4680 queries are 21 units of 224 (1568 of 1560 queries: 7) against 19 of
+// 256 with a 72-row last one, so the grids of 24 heads fill the 256 CUs more
+// evenly.  Both plans are priced with unlimited workspace so that the choice
+// does not depend on the workspace a caller passes.
+static int sp_query_tile(int B, int Mq, int H, int64_t keys) {
+  const AttnPlan p256 = attention_plan(B, Mq, H, keys, INT64_MAX, 256);
+  const AttnPlan p224 = attention_plan(B, Mq, H, keys, INT64_MAX, 224);
+  return p224.cost * (224.0 / 256.0) < p256.cost - 1e-9 ? 224 : 256;
+}
+
+static int query_tile(const wam_attention_args* a, int64_t keys) {
+  return sp_eligible(a) ? sp_query_tile(a->B, a->Mq, a->H, keys) : 256;
+}
+
+int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
+  // enough for either query tile (the call's strides, unknown here, decide)
+  return std::max(plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX, 256)),
+                  plan_bytes(attention_plan(B, Mq, H, max_keys, INT64_MAX, sp_query_tile(B, Mq, H, max_keys))));
+}
 
 int attention(const wam_attention_args* a, hipStream_t s) {
   WAM_REQUIRE(a != nullptr, "wam_attention: null args");
@@ -873,36 +914,37 @@ int attention(const wam_attention_args* a, hipStream_t s) {
                 "wam_attention: B=%d exceeds kv batch %d", a->B, a->kv_batch);
   WAM_REQUIRE(a->max_keys >= 0, "wam_attention: max_keys must be >= 0");
   if (a->Mq == 0) return WAM_OK;
-  // 8 waves (256 queries) per workgroup, with the last dispatch round split
-  // by key ranges when the plan says so and the caller gave a workspace for
-  // the partial results; small unsplit grids use 4-wave workgroups.
+  // 8 or 7 waves (256 or 224 queries) per workgroup, with the last dispatch
+  // round split by key ranges when the plan says so and the caller gave a
+  // workspace for the partial results; small grids use 4-wave workgroups.
   const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
   WAM_REQUIRE(grid8 < (1 << 26), "wam_attention: grid too large");
   const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
-  const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0);
-  // The software-pipelined kernel when every Q and own K/V row's byte
-  // offset fits in 31 bits (pool rows use 64-bit addresses).
-  const bool sp = g_attn_w4 && ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
-                  ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
-  auto sp_kernel = a->n_hist_dev ? attention_sp_kernel<true> : attention_sp_kernel<false>;
+  const bool sp = sp_eligible(a);
+  const int QT = query_tile(a, keys);
+  const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0, QT);
+  const bool hist = a->n_hist_dev != nullptr;
+  auto sp_kernel = QT == 224 ? (hist ? attention_sp_kernel<true, 7> : attention_sp_kernel<false, 7>)
+                             : (hist ? attention_sp_kernel<true, 8> : attention_sp_kernel<false, 8>);
+  const dim3 sp_block(64 * (QT / 32));
   if (p.n_split > 1) {
     float* part = static_cast<float*>(a->workspace);
     const int64_t grid = (int64_t)p.n_full + (int64_t)p.n_tail * p.n_split;
     if (sp)
-      hipLaunchKernelGGL(sp_kernel, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full, p.n_split,
-                         part);
+      hipLaunchKernelGGL(sp_kernel, dim3((unsigned)grid), sp_block, 0, s, *a, a->slots, p.n_full, p.n_split, part);
     else
       hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid), dim3(512), 0, s, *a, a->slots, p.n_full,
                          p.n_split, part);
     WAM_LAUNCHED("attention_kernel");
-    const int64_t rows = (int64_t)p.n_tail * kAttnSplitQT;
+    const int64_t rows = (int64_t)p.n_tail * QT;
     hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, *a,
-                       p.n_full, p.n_split, static_cast<const float*>(part));
+                       p.n_full, p.n_split, QT, static_cast<const float*>(part));
     WAM_LAUNCHED("attention_combine_kernel");
     return WAM_OK;
   }
-  if (sp && grid8 >= 128) {
-    hipLaunchKernelGGL(sp_kernel, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1, nullptr);
+  if (sp) {
+    const int64_t units = (int64_t)((a->Mq + QT - 1) / QT) * a->H * a->B;
+    hipLaunchKernelGGL(sp_kernel, dim3((unsigned)units), sp_block, 0, s, *a, a->slots, (int)units, 1, nullptr);
   } else if (grid8 >= 256) {
     hipLaunchKernelGGL(attention_kernel<8>, dim3((unsigned)grid8), dim3(512), 0, s, *a, a->slots, (int)grid8, 1,
                        nullptr);
@@ -957,7 +999,8 @@ int attention_noalloc(const wam_attention_args* a, hipStream_t s) {
   // whose partial results exceed the scratch are refused, not re-planned, so
   // that both entry points compute the same thing.
   const int64_t keys = a->max_keys > 0 ? a->max_keys : a->Mk;
-  const int64_t need = a->Mq > 0 ? plan_bytes(attention_plan(a->B, a->Mq, a->H, keys, INT64_MAX)) : 0;
+  const int64_t need =
+      a->Mq > 0 ? plan_bytes(attention_plan(a->B, a->Mq, a->H, keys, INT64_MAX, query_tile(a, keys))) : 0;
   WAM_REQUIRE(need <= kNoAllocScratchBytes,
               "wam_attention_noalloc: this shape's key-range split needs %lld bytes of scratch, more than "
               "the %lld-byte maximum; call wam_attention with a workspace instead",

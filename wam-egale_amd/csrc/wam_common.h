@@ -165,6 +165,13 @@ __device__ inline void asm_g_ld16_lds(uint64_t gaddr, void* lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gaddr), "{m0}"(m0) : "memory");
 }
 
+// 4 bytes per lane from a per-lane 64-bit global address into LDS
+// (global_load_lds_dword): lane L writes bytes [4 L, 4 L + 4) at `lds`.
+__device__ inline void asm_g_ld4_lds(uint64_t gaddr, void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" :: "v"(gaddr), "{m0}"(m0) : "memory");
+}
+
 // 16 bytes per lane from a buffer resource straight into LDS: lane L writes
 // bytes [16 L, 16 L + 16) of the 1 KB block at `lds` (wave-uniform).
 __device__ inline void buf_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
