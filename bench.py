@@ -221,6 +221,34 @@ def pmc_ffn1(shape, dev, M):
     print(json.dumps({"pmc_ffn1": "done", "copy_bytes": src.numel() * 2}), flush=True)
 
 
+def pmc_attn(shape, dev, M):
+    """Counter-pass workload for the attention kernels, 5 launches each, in
+    this order: self-attention over the packed QKV of the L4680 block (M
+    queries and M keys, 24 heads of 128), cross-attention of the same queries
+    over 512 text keys, and the C4a unit (1560 queries over 6240 cached pool
+    keys read through a slot list plus 1560 own keys)."""
+    import torch
+    from wam_ops import ops
+    g = torch.Generator(device=dev).manual_seed(11)
+    H, hd = shape.heads, shape.dim // shape.heads
+    r = lambda *s: torch.randn(*s, device=dev, generator=g).to(torch.bfloat16)
+    qkv = r(1, M, 3, H, hd)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    kc, vc = r(1, 512, H, hd), r(1, 512, H, hd)
+    q1, k1, v1 = r(1, 1560, H, hd), r(1, 1560, H, hd), r(1, 1560, H, hd)
+    pk, pv = r(1, 6240, H, hd), r(1, 6240, H, hd)
+    slots = torch.arange(6240, dtype=torch.int32, device=dev)
+    n_hist = torch.tensor([6240], dtype=torch.int32, device=dev)
+    for _ in range(5):
+        ops.attention(q, k, v)
+    for _ in range(5):
+        ops.attention(q, kc, vc)
+    for _ in range(5):
+        ops.attention(q1, k1, v1, pool_k=pk, pool_v=pv, slots=slots, n_hist=n_hist)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_attn": "done"}), flush=True)
+
+
 def measured_traffic():
     """HBM bytes per FFN1 launch from the committed counter summary (two
     rocprofv3 --pmc passes, each calibrated against a 1 GiB copy), or None."""
@@ -342,6 +370,9 @@ def main():
     ap.add_argument("--pmc-ffn1", action="store_true",
                     help="only launch the FFN1 GEMM 5 times and a 1 GiB device copy 3 times "
                          "(the workload for the FETCH_SIZE / WRITE_SIZE counter passes)")
+    ap.add_argument("--pmc-attn", action="store_true",
+                    help="only launch self-, cross- and C4a attention 5 times each "
+                         "(the workload for the attention instruction-count passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the block on a single MI355X "
@@ -359,6 +390,9 @@ def main():
 
     if args.pmc_ffn1:
         pmc_ffn1(shape, dev, M)
+        return
+    if args.pmc_attn:
+        pmc_attn(shape, dev, M)
         return
 
     blk = build_block(shape, dev)
