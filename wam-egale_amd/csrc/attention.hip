@@ -378,7 +378,7 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 template <bool HIST, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
                                                                   int n_full, int n_split, float* __restrict__ part) {
-  static_assert(NW == 7 || NW == 8, "7 or 8 waves");
+  static_assert(NW == 8 || (NW == 7 && !HIST), "8 waves, or 7 without pool keys");
   // three K/V stages, then (pool keys only) the 64 slots of each stage's tile
   __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage + (HIST ? 3 * kAttnKT * 4 : 0)];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -420,6 +420,8 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
     pvbase = static_cast<const bf16*>(a.pool_v) + (int64_t)prow * a.pool_bstride + h * kAttnHD;
   }
   const uint32_t kv_bytes = (uint32_t)(((int64_t)(a.Mk - 1) * a.kv_rstride + kAttnHD) * 2);
+  // bytes per pool row (the host only picks this kernel when it fits 32 bits)
+  const uint32_t pool_row_bytes = (uint32_t)a.pool_rstride * 2u;
   const i32x4 rk = make_rsrc4(kbase, kv_bytes), rv = make_rsrc4(vbase, kv_bytes);
   const bf16* qbase = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride + h * kAttnHD;
   const __amdgpu_buffer_rsrc_t rq =
@@ -475,11 +477,13 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
       } else {
         const int j = j0 + lr;
         const int slot = *reinterpret_cast<const int*>(slot_list(st_bytes) + (4 * blk + lr) * 4);
-        const bf16* pb0 = isk ? pkbase : pvbase;
-        const bf16* ob0 = isk ? kbase : vbase;
-        const char* src = reinterpret_cast<const char*>(
-            j < n_hist ? pb0 + (int64_t)slot * a.pool_rstride : ob0 + (int64_t)min(j - n_hist, a.Mk - 1) * a.kv_rstride);
-        asm_g_ld16_lds((uint64_t)(uintptr_t)(src + lc), dst);
+        // pool row: base + slot * row bytes (one 32 x 32 -> 64-bit
+        // multiply-add); own row: base + a 32-bit offset
+        const uint64_t pb0 = (uint64_t)(uintptr_t)(isk ? pkbase : pvbase) + (uint32_t)lc;
+        const uint64_t ob0 = (uint64_t)(uintptr_t)(isk ? kbase : vbase) + (uint32_t)lc;
+        const uint64_t src = j < n_hist ? pb0 + (uint64_t)(uint32_t)slot * pool_row_bytes
+                                        : ob0 + (uint32_t)(min(j - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2);
+        asm_g_ld16_lds(src, dst);
       }
     }
   };
@@ -859,28 +863,35 @@ static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_b
 static bool g_attn_w4 = true;
 
 // The pipelined kernel runs when every Q and own K/V row's byte offset fits in
-// 31 bits (pool rows use 64-bit addresses) and the query grid is at least 128
+// 31 bits (pool rows use 64-bit addresses, with a pool row's bytes in 32 bits)
+// and the query grid is at least 128
 // units of 256 rows; smaller grids use attention_kernel<4>.
 static bool sp_eligible(const wam_attention_args* a) {
   const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
   return g_attn_w4 && grid8 >= 128 && ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
-         ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX;
+         ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX &&
+         a->pool_rstride * 2 <= (int64_t)UINT32_MAX;
 }
 
-// Query rows per unit of the pipelined kernel: 224 (7 waves) when its plan,
-// in unit-times of 7/8 of a 256-row unit, costs less than the 256-row plan.
-// 4680 queries are 21 units of 224 (1568 of 1560 queries: 7) against 19 of
-// 256 with a 72-row last one, so the grids of 24 heads fill the 256 CUs more
-// evenly.  Both plans are priced with unlimited workspace so that the choice
-// does not depend on the workspace a caller passes.
+// Query rows per unit of the pipelined kernel: 224 (7 waves) when its plan
+// costs no more unit-times than the 256-row plan.  A 224-row unit takes about
+// as long as a 256-row one (the SIMDs that hold two of its waves set the
+// pace) but reads less from LDS per CU: at equal rounds it measured 1-2%
+// faster (4680 x 4680, 24 heads: 504 units of 224 or 456 of 256, both two
+// rounds of 256 CUs).  Both plans are priced with unlimited workspace so that
+// the choice does not depend on the workspace a caller passes.
 static int sp_query_tile(int B, int Mq, int H, int64_t keys) {
   const AttnPlan p256 = attention_plan(B, Mq, H, keys, INT64_MAX, 256);
   const AttnPlan p224 = attention_plan(B, Mq, H, keys, INT64_MAX, 224);
-  return p224.cost * (224.0 / 256.0) < p256.cost - 1e-9 ? 224 : 256;
+  return p224.cost <= p256.cost + 1e-9 ? 224 : 256;
 }
 
+// Calls with pool keys keep 256-query units: the pool path's per-lane 64-bit
+// addresses leave the 7-wave kernel short of registers (it spilled to scratch
+// inside the key loop), and a 224-query unit takes as long as a 256-query one
+// on the SIMDs that hold two of its waves.
 static int query_tile(const wam_attention_args* a, int64_t keys) {
-  return sp_eligible(a) ? sp_query_tile(a->B, a->Mq, a->H, keys) : 256;
+  return sp_eligible(a) && a->n_hist_dev == nullptr ? sp_query_tile(a->B, a->Mq, a->H, keys) : 256;
 }
 
 int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys) {
@@ -924,7 +935,7 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   const int QT = query_tile(a, keys);
   const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0, QT);
   const bool hist = a->n_hist_dev != nullptr;
-  auto sp_kernel = QT == 224 ? (hist ? attention_sp_kernel<true, 7> : attention_sp_kernel<false, 7>)
+  auto sp_kernel = QT == 224 ? attention_sp_kernel<false, 7>  // (never with pool keys)
                              : (hist ? attention_sp_kernel<true, 8> : attention_sp_kernel<false, 8>);
   const dim3 sp_block(64 * (QT / 32));
   if (p.n_split > 1) {
