@@ -168,9 +168,10 @@ def _ref_attn(q, k, v):
                                        (1, 4680, 512, 24), (1, 1560, 1560, 24),
                                        # grids of >= 128 workgroups of 256 queries (the
                                        # pipelined kernel): ragged queries and keys, one
-                                       # key, key-range splits
+                                       # key, key-range splits (4100 x 4099: 256-query units
+                                       # in 3 ranges; 1560 x 7800: 224-query units in 3 ranges)
                                        (2, 1000, 77, 16), (1, 3000, 1, 24), (1, 4100, 4099, 24),
-                                       (3, 700, 2500, 24), (1, 4680, 4680, 24)])
+                                       (3, 700, 2500, 24), (1, 4680, 4680, 24), (1, 1560, 7800, 24)])
 def test_attention_plain(dev, B, Mq, Mk, H):
     from wam_ops import ops
     q = _randn((B, Mq, H, 128), dev, 1)
