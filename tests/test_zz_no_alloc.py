@@ -75,6 +75,47 @@ def test_noalloc_matches_workspace_entry_point(dev):
         assert torch.equal(o_got, o_ref), f"B={B} Mq={Mq}: no-alloc output differs"
 
 
+def _args_own(q, k, v, o):
+    """Own keys only (no pool): the pipelined kernel's 224-query units."""
+    from wam_ops import _lib
+    a = _lib.AttentionArgs()
+    B, Mq, Hh, hd = q.shape
+    a.q, a.q_bstride, a.q_rstride = q.data_ptr(), q.stride(0), q.stride(1)
+    a.o, a.o_bstride, a.o_rstride = o.data_ptr(), o.stride(0), o.stride(1)
+    a.B, a.Mq, a.H, a.head_dim = B, Mq, Hh, hd
+    a.k, a.v, a.kv_bstride, a.kv_rstride = k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1)
+    a.Mk, a.kv_batch = k.shape[1], k.shape[0]
+    a.scale = 1.0 / 128 ** 0.5
+    a.max_keys = k.shape[1]
+    return a
+
+
+def test_noalloc_own_keys_split_matches(dev):
+    from wam_ops import _lib
+    from wam_ops.ops import stream_handle
+    lib = _lib.lib()
+    s = stream_handle(dev)
+    # 1560 queries over 7800 own keys, then 1300 over 3000: both plans run
+    # 224-query units in 3 key ranges (59 MB, then 50 MB of partial results)
+    for Mq, Mk, seed in ((1560, 7800, 5), (1300, 3000, 6)):
+        print(f"noalloc own-key attention Mq={Mq} Mk={Mk}", flush=True)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        r = lambda *sh: torch.randn(*sh, generator=g, device=dev).to(torch.bfloat16)
+        q, k, v = r(1, Mq, H, 128), r(1, Mk, H, 128), r(1, Mk, H, 128)
+        o_ref = torch.empty_like(q)
+        o_got = torch.full_like(q, float("nan"))
+        a = _args_own(q, k, v, o_ref)
+        need = lib.wam_attention_workspace_bytes(a.B, a.Mq, a.H, a.max_keys)
+        assert 0 < need <= 64 * MIB, need
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), need
+        assert lib.wam_attention(ctypes.byref(a), s) == _lib.WAM_OK, _err()
+        b = _args_own(q, k, v, o_got)
+        assert lib.wam_attention_noalloc(ctypes.byref(b), s) == _lib.WAM_OK, _err()
+        torch.cuda.synchronize()
+        assert torch.equal(o_got, o_ref), f"Mq={Mq} Mk={Mk}: no-alloc output differs"
+
+
 def test_noalloc_refuses_on_host(dev):
     from wam_ops import _lib
     from wam_ops.ops import stream_handle
