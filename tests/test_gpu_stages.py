@@ -181,6 +181,37 @@ def test_attention_plain(dev, B, Mq, Mk, H):
     assert_close(o, _ref_attn(q, k, v), 2e-2, 0.9999, f"attention {B}x{Mq}x{Mk}x{H}")
 
 
+@pytest.mark.parametrize("B,Mq,Mk,H,nvalid", [(1, 100, 300, 2, 0), (1, 4680, 4680, 24, 0),
+                                              (1, 1560, 7800, 24, 0), (2, 1000, 3000, 24, 1237),
+                                              (1, 1560, 1560, 24, 6240)])
+def test_attention_rising_scores(dev, B, Mq, Mk, H, nvalid):
+    """Scores that rise along the keys, so the running max moves many times.
+
+    Key j is scaled by 1 + 40 j / n (score spread from about 1 to 41 natural
+    units).  A block of 64 keys three fifths of the way along is scaled by
+    100 on top of that: its scores sit hundreds of log2 units above the max
+    of the keys before it, past the range of an fp32 exponential taken
+    against that max.  nvalid > 0 puts the first nvalid keys in a pool read
+    through a slot list.
+    """
+    from wam_ops import ops
+    n = nvalid + Mk
+    ramp = 1 + 40 * torch.arange(n, device=dev, dtype=torch.float32) / n
+    j0 = (3 * n) // 5
+    ramp[j0:j0 + 64] *= 100
+    q = _randn((B, Mq, H, 128), dev, 1)
+    kall = (_randn((B, n, H, 128), dev, 2).float() * ramp[None, :, None, None]).bfloat16()
+    vall = _randn((B, n, H, 128), dev, 3)
+    if nvalid:
+        slots = torch.arange(nvalid, dtype=torch.int32, device=dev)
+        o = ops.attention(q, kall[:, nvalid:], vall[:, nvalid:], pool_k=kall[:, :nvalid].contiguous(),
+                          pool_v=vall[:, :nvalid].contiguous(), slots=slots,
+                          n_hist=torch.tensor([nvalid], dtype=torch.int32, device=dev))
+    else:
+        o = ops.attention(q, kall, vall)
+    assert_close(o, _ref_attn(q, kall, vall), 2e-2, 0.9999, f"rising scores {B}x{Mq}x{Mk}+{nvalid}")
+
+
 def test_attention_strided_and_broadcast(dev):
     from wam_ops import ops
     B, M, H = 2, 70, 2

@@ -1082,8 +1082,11 @@ static bool w4_t224_wins(int M, int seg_n, int n_seg, int K, int cus, int64_t ws
   double c256 = (double)((t256 + cus - 1) / cus);
   const GemmPlan g = gemm_plan(M, seg_n, n_seg, K, cus, ws_bytes);
   if (g.kind != 0) {
-    // the plan's tail costs at most what it replaces; count it as a quarter round
-    c256 = (double)(t256 / cus) + 0.25;
+    // The plan's tail, in full-tile rounds: 0.4, as measured for the 128x128
+    // tail of 4680 x 14336 x 3072 (35 us against 87 us per round of 256-row
+    // tiles).  That shape then takes the 224-row tiles, whose partial fifth
+    // round runs at a higher clock than the full ones.
+    c256 = (double)(t256 / cus) + 0.4;
   }
   const double c224 = (double)((t224 + cus - 1) / cus) * (224.0 / 256.0);
   return c224 < c256 - 1e-9;
