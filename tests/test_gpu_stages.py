@@ -50,10 +50,11 @@ def test_linear_bias(dev, M, K, N, nseg):
         assert_close(o, ref, max_abs=bound, min_cos=0.99999, what=f"linear {M}x{K}x{N}")
 
 
-# (4680, 256, 3584) and (4680, 256, 14336) have 266 and 1064 256x256 tiles:
-# just above a multiple of the 256 CUs, so their last columns run as a second
-# 128x128-tile launch (column offsets into bias, residual, output and the
-# modulation table).  (6240, 3072, 2816) and (6240, 6144, 3072) run their last
+# (4680, 256, 3584) has 266 256x256 tiles, just above a multiple of the 256
+# CUs, so its last columns run as a second 128x128-tile launch (column offsets
+# into bias, residual, output and the modulation table); (4680, 256, 14336)
+# (1064 such tiles) runs on 224-row tiles instead, which take 4.375 rounds
+# against 4 rounds and a tail counted as 0.4.  (6240, 3072, 2816) and (6240, 6144, 3072) run their last
 # columns split over k (8 and 5 ranges of fp32 partials, then a reduce pass
 # with the epilogue); (3900, 4160, 4352) does so with a partial last row tile
 # and 65 k-tiles in 8 uneven ranges.  (300, 512, 200) ends in a partial
