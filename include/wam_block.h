@@ -135,6 +135,24 @@ typedef struct {
    * seg_n, n_seg, K) bytes), or, without it, as smaller tiles.  Not in the
    * reference (cuBLASLt picks its own algorithm and workspace). */
   void* workspace; int64_t workspace_bytes;
+  /* Optional q/k-norm epilogue (WAM_EPI_BIAS only): the across-heads RMSNorm
+   * and RoPE of model.py:609-623 (replacing the separate norm_q/norm_k + rope
+   * passes, baseline/csrc/block.cu:103-118), split so that a 256-column tile
+   * can apply them.  For each segment s with norm_ssq[s] != NULL, with
+   * y = bf16(acc + b) of row m:
+   *   norm_ssq[s][m * ceil(seg_n / 256) + c / 256] = sum of y^2 over the 256
+   *     columns of group c / 256 (fp32),
+   *   out = bf16(rope(y * norm_gamma[s]))  (bf16 gamma [seg_n]; rotation of
+   *     pairs (2j, 2j+1) of every norm_head_dim-wide head by
+   *     norm_freq[fb, t, j], complex64 [norm_freq_batch, norm_tokens,
+   *     norm_head_dim / 2], row m = b * norm_tokens + t; no rotation when
+   *     norm_freq is NULL).
+   * The 1/rms factor rsqrt(sum of the row's norm_ssq / seg_n + eps) is left
+   * to the consumer (wam_attention's q_ssq; the rotation is linear, so it
+   * commutes with that factor).  Not in the reference, whose norm is a
+   * separate row pass. */
+  float* norm_ssq[3]; const void* norm_gamma[3];
+  const void* norm_freq; int norm_freq_batch, norm_tokens, norm_head_dim;
 } wam_linear_args;
 
 int wam_linear(const wam_linear_args* args, void* stream);
@@ -205,6 +223,12 @@ typedef struct {
    * only to plan the split.  Not in the reference (its FlashAttention call
    * chooses splits internally). */
   void* workspace; int64_t workspace_bytes; int max_keys;
+  /* Optional per-query RMS factor, for queries written by wam_linear's norm
+   * epilogue: when q_ssq != NULL, query row r = b * Mq + i is taken as
+   * Q[b, i] * rsqrt(sum_{t < q_ssq_n} q_ssq[r * q_ssq_n + t] / q_norm_dim
+   * + q_eps), applied to its scores (which are linear in Q).  q_ssq_n <= 16.
+   * The reference normalises Q in a separate pass (model.py:609-612). */
+  const float* q_ssq; int q_ssq_n; int q_norm_dim; float q_eps;
 } wam_attention_args;
 
 int wam_attention(const wam_attention_args* args, void* stream);

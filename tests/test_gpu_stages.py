@@ -160,6 +160,61 @@ def test_rms_rope(dev, B, M, H):
     assert_close(q2, ref, _ulp_bound(ref), 0.99999, "rms in place")
 
 
+# The q/k-norm epilogue of the projection: checked against the plain bias
+# GEMM's own bf16 output y (same kernels, same accumulation), so both the
+# sums of squares and bf16(rope(y * gamma)) have exact references.  4680
+# rows end in the four-wave kernel (224-row tiles; three segments = QKV, one
+# = cross q); 520 and 120 rows in other tile kernels plus the norm pass; 6240
+# rows = 4 samples of 1560 tokens sharing one RoPE table (row modulo tokens).
+@pytest.mark.parametrize("M,nseg,grid", [(4680, 3, (6, 26, 30)), (4680, 1, None), (520, 3, (2, 10, 26)),
+                                         (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30))])
+def test_linear_qk_norm(dev, M, nseg, grid):
+    from wam_ops import ops, synthetic
+    K = N = 3072
+    H = N // 128
+    x = _randn((M, K), dev, 1)
+    ws = [_randn((N, K), dev, 10 + i, 0.02) for i in range(nseg)]
+    bs = [_randn((N,), dev, 20 + i, 0.02) for i in range(nseg)]
+    gs = [_randn((N,), dev, 30 + i, 0.1) + 1 for i in range(min(nseg, 2))] + [None] * (nseg - 2)
+    freq = synthetic.rope_freqs(synthetic.mesh_grid_ids(*grid)).to(dev) if grid else None
+    plain = ops.linear(x, ws, bs)
+    outs, ssqs = ops.linear(x, ws, bs, norm_gamma=gs, norm_freq=freq)
+    for i in range(nseg):
+        if gs[i] is None:
+            assert ssqs[i] is None and torch.equal(outs[i], plain[i]), "segment without norm = plain GEMM"
+            continue
+        y = plain[i].float()
+        ref_ss = (y.double() ** 2).reshape(M, N // 256, 256).sum(-1)
+        rel = ((ssqs[i].double() - ref_ss).abs() / ref_ss).max().item()
+        print(f"qk-norm {M}x{nseg} seg {i}: sum of squares rel err {rel:.2e}")
+        assert rel < 1e-5, rel
+        z = y * gs[i].float()
+        if freq is not None:
+            z = apply_rope(z.reshape(-1, freq.shape[1], H, 128), freq).reshape(M, N)
+        ref = z.float()
+        same = (outs[i] == ref.to(torch.bfloat16)).float().mean().item()
+        assert same > 0.999, f"only {same:.5f} of the outputs equal bf16(rope(y * gamma))"
+        assert_close(outs[i], ref, _ulp_bound(ref, 1e-3), 0.99999, f"qk-norm out {M}x{nseg} seg {i}")
+
+
+@pytest.mark.parametrize("B,Mq,Mk,H", [(2, 100, 37, 2), (1, 4680, 4680, 24), (1, 4680, 512, 24),
+                                       (1, 1560, 7800, 24)])
+def test_attention_q_ssq(dev, B, Mq, Mk, H):
+    """Queries scaled by their 1/rms inside attention (q_ssq) against
+    attention over the RMS-normalised queries."""
+    from wam_ops import ops
+    D = H * 128
+    y = _randn((B, Mq, D), dev, 1, 3.0)
+    g = _randn((D,), dev, 4, 0.1) + 1
+    k = _randn((B, Mk, H, 128), dev, 2)
+    v = _randn((B, Mk, H, 128), dev, 3)
+    yf = y.float()
+    ssq = (yf ** 2).reshape(B * Mq, -1, min(D, 256)).sum(-1).contiguous()
+    qg = (yf * g.float()).to(torch.bfloat16).reshape(B, Mq, H, 128)
+    o = ops.attention(qg, k, v, q_ssq=ssq, q_eps=1e-6)
+    qn = torch.nn.functional.rms_norm(yf, (D,), g.float(), 1e-6).reshape(B, Mq, H, 128)
+    assert_close(o, _ref_attn(qn, k, v), 2e-2, 0.9999, f"attention q_ssq {B}x{Mq}x{Mk}x{H}")
+
 def _ref_attn(q, k, v):
     return torch.nn.functional.scaled_dot_product_attention(
         q.float().transpose(1, 2), k.float().transpose(1, 2), v.float().transpose(1, 2)).transpose(1, 2)

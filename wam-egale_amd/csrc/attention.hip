@@ -43,6 +43,34 @@ __device__ inline int v_off(int key, int c) { return key * 256 + ((c ^ ((key & 3
 
 __device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n - 1 : r); }
 
+// Per-query RMS factor of queries written by wam_linear's norm epilogue:
+// rsqrt(sum of the row's q_ssq_n partial sums of squares / q_norm_dim + eps)
+// for query row b * Mq + qi (clamped into range).  The RMSNorm across heads
+// is model.py:609-612; the rotation after it is linear and commutes.
+constexpr int kQssqMax = 16;
+// The loads are unconditional (clamped index, then a select), so that no
+// branch separates them from the code after them.
+__device__ inline void q_ssq_load(const wam_attention_args& a, int b, int qi, float qp[kQssqMax]) {
+  const float* p = a.q_ssq + ((int64_t)b * a.Mq + min(qi, a.Mq - 1)) * a.q_ssq_n;
+  const int last = a.q_ssq_n - 1;
+#pragma unroll
+  for (int t = 0; t < kQssqMax; ++t) {
+    const float v = p[min(t, last)];
+    qp[t] = t <= last ? v : 0.f;
+  }
+}
+__device__ inline float q_ssq_factor(const wam_attention_args& a, const float qp[kQssqMax]) {
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < kQssqMax; ++t) s += qp[t];
+  return rsqrtf(s / (float)a.q_norm_dim + a.q_eps);
+}
+__device__ inline float q_rms_factor(const wam_attention_args& a, int b, int qi) {
+  float qp[kQssqMax];
+  q_ssq_load(a, b, qi, qp);
+  return q_ssq_factor(a, qp);
+}
+
 // Workgroup: W waves x 32 queries of one (batch row, head).  Wave w owns
 // queries q0 + 32 w .. +32 and keeps its Q fragments in registers.
 // A unit is one (query tile, batch row, head), numbered query tile fastest.
@@ -150,7 +178,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
     }
   };
 
-  const float sc = a.scale * kLog2e;
+  float sc = a.scale * kLog2e;
+  if (a.q_ssq) sc *= q_rms_factor(a, b, qi);
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[4];
 #pragma unroll
@@ -493,7 +522,9 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
     else __builtin_amdgcn_s_waitcnt(5 | (7 << 4) | (15 << 8));
   };
 
-  const float sc = a.scale * kLog2e;
+  // Softmax scale in log2 units; with q_ssq, times the query's 1/rms (set in
+  // the prologue, once the partial sums have had the first tile's time to land).
+  float sc = a.scale * kLog2e;
   const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[4];
@@ -677,10 +708,15 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
     }
     issue(t_first, 0);
     if (ntiles > 1) issue(t_first + 1, kAttnStage);
+    // (loaded after the tile loads: the wait for them then falls on the
+    // first step's own wait for tile 1)
+    float qp[kQssqMax];
+    if (a.q_ssq) q_ssq_load(a, b, qi, qp);
     if (ntiles > 1) wait_all_but_one_tile();
     else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __builtin_amdgcn_s_barrier();
     s_mfma(0, s0);
+    if (a.q_ssq) sc *= q_ssq_factor(a, qp);
     // Stages of tiles t, t+1 and t+2, rotated each step (scalar values; an
     // expression in t would become per-lane induction variables).
     int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
@@ -924,6 +960,9 @@ int attention(const wam_attention_args* a, hipStream_t s) {
     WAM_REQUIRE(a->B <= a->kv_batch || a->kv_batch == 1,
                 "wam_attention: B=%d exceeds kv batch %d", a->B, a->kv_batch);
   WAM_REQUIRE(a->max_keys >= 0, "wam_attention: max_keys must be >= 0");
+  WAM_REQUIRE(!a->q_ssq || (a->q_ssq_n >= 1 && a->q_ssq_n <= kQssqMax && a->q_norm_dim >= 1),
+              "wam_attention: q_ssq needs 1..%d partials per row and q_norm_dim >= 1 (got %d, %d)", kQssqMax,
+              a->q_ssq_n, a->q_norm_dim);
   if (a->Mq == 0) return WAM_OK;
   // 8 or 7 waves (256 or 224 queries) per workgroup, with the last dispatch
   // round split by key ranges when the plan says so and the caller gave a

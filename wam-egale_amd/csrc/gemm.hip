@@ -36,9 +36,15 @@ struct LinearParams {
   // the ranges in order and applies the epilogue.
   int k_split;
   float* part;
+  // q/k-norm epilogue (kEpiBiasNorm): per segment, the sums of squares of
+  // the bf16 outputs per 256-column group (row stride ssq_ld), the gamma the
+  // outputs are multiplied by, and the RoPE table (nfreq, or none).
+  float* ssq[3]; const bf16* ngamma[3];
+  const float2* nfreq; int nfreq_batch, ntokens, nhd, ssq_ld;
 };
 
-constexpr int kEpiPartial = 100;  // kernel epilogue of a split-K range: raw fp32 sums
+constexpr int kEpiPartial = 100;   // kernel epilogue of a split-K range: raw fp32 sums
+constexpr int kEpiBiasNorm = 101;  // bias, then the q/k-norm epilogue (four-wave kernel only)
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0,
           int WB_ = 2, int SPLIT_ = 1>
@@ -759,10 +765,34 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     const int rr = ps * 4 + (tid >> 6);
     return TM == 256 ? (rr >> 6) * 128 + 64 * r + (rr & 63) : 128 * r + rr;
   };
+  // The same row from the wave-uniform wave index (scalar arithmetic).
+  auto row_u = [&](int r, int ps) {
+    const int rr = ps * 4 + wave;
+    return TM == 256 ? (rr >> 6) * 128 + 64 * r + (rr & 63) : 128 * r + rr;
+  };
+  // q/k-norm epilogue of this segment: gamma of the lane's 4 columns, the
+  // RoPE pair index of its first column, and the tile's 256-column group.
+  constexpr bool NORM = EPI == kEpiBiasNorm;
+  float* const nssq = NORM ? (seg == 0 ? p.ssq[0] : (seg == 1 ? p.ssq[1] : p.ssq[2])) : nullptr;
+  const bool nrm = NORM && nssq != nullptr;
+  const bool rope = nrm && p.nfreq != nullptr;
+  float gm[4] = {1.f, 1.f, 1.f, 1.f};
+  if (nrm) {
+    const bf16* g = seg == 0 ? p.ngamma[0] : (seg == 1 ? p.ngamma[1] : p.ngamma[2]);
+    const bf16x4 tg = *reinterpret_cast<const bf16x4*>(g + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gm[e] = static_cast<float>(tg[e]);
+  }
+  const int jp = rope ? (n % p.nhd) >> 1 : 0;
+  const int gcol = n0 >> 8;
   // One round; r is a compile-time constant, so the pass loops below unroll
   // and the residual registers are never indexed at run time.
-  auto round = [&](auto r_c) {
+  // RoPE table row of tile row `row` (wave-uniform): the row itself, or the
+  // row modulo the tokens of one sample when every sample shares the table.
+  const int fmod = (NORM && p.nfreq_batch == 1 && p.ntokens < p.M) ? p.ntokens : 0;
+  auto round = [&](auto r_c, auto nrm_c, auto rope_c) {
     constexpr int r = decltype(r_c)::value;
+    constexpr bool NRM = decltype(nrm_c)::value, ROPE = decltype(rope_c)::value;
     constexpr int nps = (TM == 224 && r == 1) ? 24 : 32;
     u32x4v rraw[RES ? 32 : 1];
     if constexpr (RES) {
@@ -775,6 +805,37 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           const u32x2v t2 = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rres, off, 0, 0));
           rraw[ps] = u32x4v{t2[0], t2[1], 0u, 0u};
         }
+      }
+    }
+    // The round's RoPE factors (two complex per lane and row), in flight
+    // during the LDS exchange like the residual rows.
+    float4 fr[ROPE ? 32 : 1];
+    if constexpr (ROPE) {
+      // Rows of the round are row_u(r, 0) + offsets below 256; with a shared
+      // table one division per round, then at most one wrap per row when a
+      // sample has >= 256 tokens.
+      const int base = m0 + row_u(r, 0);
+      // buffer loads: the lane's pair offset in the address, the (uniform)
+      // row offset in the scalar offset
+      const int hb = (p.nhd >> 1) * 8;
+      const __amdgpu_buffer_rsrc_t rf =
+          make_rsrc(p.nfreq, (uint32_t)(p.nfreq_batch == 1 ? p.ntokens : p.M) * (uint32_t)hb);
+      auto ld = [&](int ps, int frow) {
+        fr[ps] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rf, jp * 8, frow * hb, 0));
+      };
+      if (fmod == 0) {
+#pragma unroll
+        for (int ps = 0; ps < nps; ++ps) ld(ps, min(base + row_u(r, ps) - row_u(r, 0), p.M - 1));
+      } else if (fmod >= 256) {
+        const int tb = base % fmod;
+#pragma unroll
+        for (int ps = 0; ps < nps; ++ps) {
+          const int t = tb + row_u(r, ps) - row_u(r, 0);
+          ld(ps, t >= fmod ? t - fmod : t);
+        }
+      } else {
+#pragma unroll
+        for (int ps = 0; ps < nps; ++ps) ld(ps, (base + row_u(r, ps) - row_u(r, 0)) % fmod);
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -806,6 +867,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
 #pragma unroll
     for (int b8 = 0; b8 < nps / 8; ++b8) {
       f32x4 vv[8];
+      float ssr[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k8 = 0; k8 < 8; ++k8) {
         const int ps = b8 * 8 + k8;
@@ -865,15 +927,62 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           bf16x4 o;
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(y[e]);
+          if constexpr (NRM) {
+            // y = bf16(acc + b): its squares, then gamma and the rotation of
+            // pairs (n, n+1), (n+2, n+3) in fp32, one rounding.
+            float z[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) z[e] = static_cast<float>(o[e]);
+            const bf16x2 o01 = {o[0], o[1]}, o23 = {o[2], o[3]};
+            ssr[k8] = __builtin_amdgcn_fdot2_f32_bf16(o23, o23, __builtin_amdgcn_fdot2_f32_bf16(o01, o01, 0.f, false),
+                                                      false);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) z[e] *= gm[e];
+            if constexpr (ROPE) {
+              const float4 f = fr[ps];
+              const float a0 = z[0] * f.x - z[1] * f.y, a1 = z[0] * f.y + z[1] * f.x;
+              const float a2 = z[2] * f.z - z[3] * f.w, a3 = z[2] * f.w + z[3] * f.z;
+              z[0] = a0; z[1] = a1; z[2] = a2; z[3] = a3;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(z[e]);
+          }
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2v, o), rout, off, 0, 0);
+        }
+      }
+      if constexpr (NRM) {
+        // The 8 rows' sums over the wave's 256 columns: lane 16 g + 0 holds
+        // rows 2 (g & 1) + 4 (g >> 1) + j of the batch in red[j].
+        float red[2];
+        wave_sum8(ssr, red);
+        const int g = lane >> 4;
+        if ((lane & 15) == 0) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int mrow = m0 + row_of(r, b8 * 8 + 2 * (g & 1) + 4 * (g >> 1) + j);
+            if (mrow < p.M) nssq[(int64_t)mrow * p.ssq_ld + gcol] = red[j];
+          }
         }
       }
       // one batch of LDS reads live at a time
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  round(std::integral_constant<int, 0>{});
-  round(std::integral_constant<int, 1>{});
+  // Both rounds per variant: the norm variants are chosen once per tile (a
+  // segment's tiles all take one), so no per-row branch remains.
+  auto rounds = [&](auto nrm_c, auto rope_c) {
+    round(std::integral_constant<int, 0>{}, nrm_c, rope_c);
+    round(std::integral_constant<int, 1>{}, nrm_c, rope_c);
+  };
+  using F = std::false_type;
+  using T = std::true_type;
+  if constexpr (NORM) {
+    if (rope) rounds(T{}, T{});
+    else if (nrm) rounds(T{}, F{});
+    else rounds(F{}, F{});
+  } else {
+    rounds(F{}, F{});
+  }
 }
 
 // Tile configurations: BM x BN x BK, waves (M x N), LDS stages.
@@ -923,6 +1032,53 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p)
     }
   }
   epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false, rv);
+}
+
+// The q/k-norm epilogue as a pass over a finished bias GEMM's bf16 output,
+// for launches that do not end in the four-wave kernel: one wave per (row,
+// 256-column group) of segment `seg`, the arithmetic of kEpiBiasNorm.
+__global__ __launch_bounds__(256) void linear_norm_kernel(LinearParams p, int seg) {
+  const int lane = threadIdx.x & 63;
+  const int64_t job = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (job >= (int64_t)p.M * p.ssq_ld) return;
+  const int m = (int)(job / p.ssq_ld), g = (int)(job - (int64_t)m * p.ssq_ld);
+  const int n = g * 256 + 4 * lane;
+  const bool ok = n < p.seg_n;  // seg_n is a multiple of 8: whole groups of 4
+  bf16* out = static_cast<bf16*>(seg == 0 ? p.out[0] : (seg == 1 ? p.out[1] : p.out[2])) + (int64_t)m * p.ldo;
+  float z[4] = {0.f, 0.f, 0.f, 0.f};
+  if (ok) {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(out + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) z[e] = static_cast<float>(t[e]);
+  }
+  const float ss = wave_sum(z[0] * z[0] + z[1] * z[1] + z[2] * z[2] + z[3] * z[3]);
+  float* ssq = seg == 0 ? p.ssq[0] : (seg == 1 ? p.ssq[1] : p.ssq[2]);
+  if (lane == 0) ssq[(int64_t)m * p.ssq_ld + g] = ss;
+  if (!ok) return;
+  const bf16x4 tg = *reinterpret_cast<const bf16x4*>((seg == 0 ? p.ngamma[0] : (seg == 1 ? p.ngamma[1] : p.ngamma[2])) + n);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) z[e] *= static_cast<float>(tg[e]);
+  if (p.nfreq) {
+    const int frow = (p.nfreq_batch == 1 && p.ntokens < p.M) ? m % p.ntokens : m;
+    const float4 f = *reinterpret_cast<const float4*>(p.nfreq + (int64_t)frow * (p.nhd >> 1) + ((n % p.nhd) >> 1));
+    const float a0 = z[0] * f.x - z[1] * f.y, a1 = z[0] * f.y + z[1] * f.x;
+    const float a2 = z[2] * f.z - z[3] * f.w, a3 = z[2] * f.w + z[3] * f.z;
+    z[0] = a0; z[1] = a1; z[2] = a2; z[3] = a3;
+  }
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(z[e]);
+  *reinterpret_cast<bf16x4*>(out + n) = o;
+}
+
+static int linear_norm_pass(const LinearParams& p, hipStream_t s) {
+  const int64_t jobs = (int64_t)p.M * p.ssq_ld;
+  for (int i = 0; i < p.n_seg_count; ++i) {
+    if (!p.ssq[i]) continue;
+    hipLaunchKernelGGL(linear_norm_kernel, dim3((unsigned)((jobs + 3) / 4)), dim3(256), 0, s, p, i);
+    WAM_LAUNCHED("linear_norm_kernel");
+  }
+  return WAM_OK;
 }
 
 template <class C, int EPI>
@@ -981,6 +1137,10 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
     return WAM_OK;
   }
   switch (p.epi) {
+    case kEpiBiasNorm:
+      if constexpr (C::kW4) launch_tiles<C, kEpiBiasNorm>(dim3(grid), p, s);
+      else WAM_REQUIRE(false, "wam_linear: the q/k-norm epilogue runs in the four-wave kernel only");
+      break;
     case WAM_EPI_BIAS:
       launch_tiles<C, WAM_EPI_BIAS>(dim3(grid), p, s);
       break;
@@ -1157,6 +1317,29 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   p.k_split = 1;
   p.part = static_cast<float*>(a->workspace);
   const int64_t ws_bytes = a->workspace ? a->workspace_bytes : 0;
+  const bool norm = a->norm_ssq[0] || a->norm_ssq[1] || a->norm_ssq[2];
+  if (norm) {
+    WAM_REQUIRE(a->epilogue == WAM_EPI_BIAS && !f8 && a->out_dtype == WAM_BF16,
+                "wam_linear: the q/k-norm epilogue needs WAM_EPI_BIAS, bf16 weights and a bf16 output");
+    for (int i = 0; i < 3; ++i) {
+      WAM_REQUIRE(!a->norm_ssq[i] || (i < a->n_seg && a->norm_gamma[i]),
+                  "wam_linear: norm segment %d needs a gamma (and must exist)", i);
+      p.ssq[i] = i < a->n_seg ? a->norm_ssq[i] : nullptr;
+      p.ngamma[i] = i < a->n_seg ? static_cast<const bf16*>(a->norm_gamma[i]) : nullptr;
+    }
+    if (a->norm_freq) {
+      WAM_REQUIRE(a->norm_head_dim > 0 && a->norm_head_dim % 4 == 0 && a->seg_n % a->norm_head_dim == 0,
+                  "wam_linear: norm head_dim %d must be a multiple of 4 dividing N=%d", a->norm_head_dim,
+                  a->seg_n);
+      WAM_REQUIRE(a->norm_tokens >= 1 && a->M % a->norm_tokens == 0 &&
+                  (a->norm_freq_batch == 1 || a->norm_freq_batch == a->M / a->norm_tokens),
+                  "wam_linear: norm freq batch %d / tokens %d contract", a->norm_freq_batch, a->norm_tokens);
+      WAM_REQUIRE(((uintptr_t)a->norm_freq & 15) == 0, "wam_linear: norm_freq must be 16-byte aligned");
+      p.nfreq = static_cast<const float2*>(a->norm_freq);
+      p.nfreq_batch = a->norm_freq_batch; p.ntokens = a->norm_tokens; p.nhd = a->norm_head_dim;
+    }
+    p.ssq_ld = (a->seg_n + 255) / 256;
+  }
   const bool big = uses_big_tiles(a->M, a->seg_n, a->n_seg);
   if (f8) {
     if (big) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, ws_bytes, s);
@@ -1171,16 +1354,26 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   // than the loop gains when the loop is short (4680 and 6240 x 3072 x 3072
   // with the gated and plain residual epilogues: 4-12% slower than the
   // eight-wave kernel; every other block GEMM 0-10% faster).
+  // With the q/k-norm epilogue, a launch that is one four-wave grid applies
+  // it in its epilogue; any other runs the bias GEMM and then the norm pass.
   if (big) {
     const bool res = a->epilogue == WAM_EPI_BIAS_GATE_RES || a->epilogue == WAM_EPI_BIAS_RES;
-    if (w4_t224_wins(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes))
+    if (w4_t224_wins(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes)) {
+      if (norm) p.epi = kEpiBiasNorm;
       return launch_gemm<CfgW4t224>(p, s);
+    }
     if (res && a->K <= 4096) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
-    return launch_big<CfgW4, Cfg128x128w4>(p, ws_bytes, s);
+    if (norm && gemm_plan(p.M, p.seg_n, p.n_seg_count, p.K, device_cu_count(), p.part ? ws_bytes : 0).kind == 0) {
+      p.epi = kEpiBiasNorm;
+      return launch_gemm<CfgW4>(p, s);
+    }
+    WAM_TRY((launch_big<CfgW4, Cfg128x128w4>(p, ws_bytes, s)));
+    return norm ? linear_norm_pass(p, s) : WAM_OK;
   }
   const int64_t mid_tiles = (int64_t)((a->M + 255) / 256) * (a->seg_n / 128) * a->n_seg;
-  if (mid_tiles >= 200) return launch_gemm<Cfg256x128w4>(p, s);
-  return launch_gemm<Cfg128x128w4>(p, s);
+  if (mid_tiles >= 200) WAM_TRY(launch_gemm<Cfg256x128w4>(p, s));
+  else WAM_TRY(launch_gemm<Cfg128x128w4>(p, s));
+  return norm ? linear_norm_pass(p, s) : WAM_OK;
 }
 
 // Per-row fp8 e4m3 quantization: one workgroup per row.

@@ -266,6 +266,32 @@ __device__ inline float wave_sum(float v) {
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
 }
 
+// Eight sums over the 64 lanes of a wave at once: v[k] summed over all lanes
+// lands in out[j] for k = j + 2 (r & 1) + 4 (r >> 1), r = lane / 16, on all
+// 16 lanes of row r.  Two halving exchanges (v_permlane32_swap trades the
+// upper 32 lanes of its first operand for the lower 32 of its second, so the
+// sum of the two results holds v[j] in lanes 0-31 and v[j + 4] in 32-63;
+// v_permlane16_swap does the same with odd and even 16-lane rows), then
+// rotations within the rows of 16: 20 instructions for 8 sums.
+__device__ inline void wave_sum8(const float v[8], float out[2]) {
+  float t[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 4]), false, false);
+    t[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t[j]), __float_as_uint(t[j + 2]), false, false);
+    float s = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    s += dpp<0x128>(s);  // row_ror:8
+    s += dpp<0x124>(s);  // row_ror:4
+    s += dpp<0x4E>(s);   // quad_perm [2, 3, 0, 1]
+    s += dpp<0xB1>(s);   // quad_perm [1, 0, 3, 2]
+    out[j] = s;
+  }
+}
+
 // GELU, tanh approximation: 0.5 x (1 + tanh(u)) = x * sigmoid(2u),
 // u = sqrt(2/pi) (x + 0.044715 x^3).  sigmoid via v_exp_f32 and v_rcp_f32.
 __device__ inline float gelu_tanh(float x) {

@@ -42,7 +42,9 @@ class LinearArgs(Structure):
                 ("res_dtype", c_int), ("out_dtype", c_int),
                 ("gate", Modulation), ("gate_index", c_int),
                 ("w_dtype", c_int), ("w_scale", c_void_p * 3),
-                ("workspace", c_void_p), ("workspace_bytes", c_int64)]
+                ("workspace", c_void_p), ("workspace_bytes", c_int64),
+                ("norm_ssq", c_void_p * 3), ("norm_gamma", c_void_p * 3), ("norm_freq", c_void_p),
+                ("norm_freq_batch", c_int), ("norm_tokens", c_int), ("norm_head_dim", c_int)]
 
 
 class LnArgs(Structure):
@@ -67,7 +69,8 @@ class AttentionArgs(Structure):
                 ("n_hist_dev", c_void_p), ("pool_rows", c_void_p), ("k", c_void_p),
                 ("v", c_void_p), ("kv_bstride", c_int64), ("kv_rstride", c_int64),
                 ("Mk", c_int), ("kv_rows", c_void_p), ("kv_batch", c_int), ("scale", c_float),
-                ("workspace", c_void_p), ("workspace_bytes", c_int64), ("max_keys", c_int)]
+                ("workspace", c_void_p), ("workspace_bytes", c_int64), ("max_keys", c_int),
+                ("q_ssq", c_void_p), ("q_ssq_n", c_int), ("q_norm_dim", c_int), ("q_eps", c_float)]
 
 
 class KvLayoutArgs(Structure):

@@ -103,13 +103,21 @@ def quantize_fp8_rows(w, out=None, scale=None):
 
 
 def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=None,
-           temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16, w_scale=None):
+           temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16, w_scale=None,
+           norm_gamma=None, norm_freq=None, norm_head_dim=128):
     """Y = epilogue(x W^T + b) on MFMA.  weights: one tensor or a list of up to 3
     (one launch, outputs split per weight).  Returns a tensor or a list.
     The residual may be bf16 or fp32; out_dtype=float32 is allowed for the
     residual epilogues (the block keeps its residual stream in fp32).
     Weights may be float8_e4m3fn with per-output-column fp32 w_scale (one
-    tensor or a list matching the weights): y = acc * w_scale + b."""
+    tensor or a list matching the weights): y = acc * w_scale + b.
+
+    norm_gamma (the q/k-norm epilogue; one bf16 [N] tensor or None per
+    segment): segment i with a gamma returns bf16(rope(y * gamma)) with
+    y = bf16(x W^T + b), rotated by norm_freq (complex64 [Bf, tokens, 1 or
+    absent, head_dim / 2], or None), and the call returns (outputs, sums)
+    where sums[i] is the fp32 [M, ceil(N / 256)] sum of y^2 per row and
+    256-column group (None for segments without a gamma)."""
     single = torch.is_tensor(weights)
     ws = [weights] if single else list(weights)
     bs = [biases] if (single or biases is None) else list(biases)
@@ -161,6 +169,28 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         for i, sc in enumerate(scs):
             a.w_scale[i] = sc.data_ptr()
     a.out_dtype = dtype_code(outs[0])
+    ssqs = None
+    if norm_gamma is not None:
+        gs = [norm_gamma] if torch.is_tensor(norm_gamma) else list(norm_gamma)
+        _req(len(gs) == len(ws) and any(g is not None for g in gs), "one norm gamma (or None) per segment")
+        ssqs = []
+        for i, g in enumerate(gs):
+            if g is None:
+                ssqs.append(None)
+                continue
+            _bf16(g, "norm gamma")
+            _req(g.is_contiguous() and g.numel() == N and g.device == dev, "norm gamma must be [N]")
+            sq = torch.empty(M, (N + 255) // 256, dtype=torch.float32, device=dev)
+            a.norm_ssq[i], a.norm_gamma[i] = sq.data_ptr(), g.data_ptr()
+            ssqs.append(sq)
+        if norm_freq is not None:
+            _req(norm_freq.dtype == torch.complex64 and norm_freq.is_contiguous() and norm_freq.device == dev,
+                 "norm_freq must be contiguous complex64 on the device")
+            _req(norm_freq.shape[-1] == norm_head_dim // 2, "norm_freq must be [Bf, tokens, 1, hd/2]")
+            toks = norm_freq.shape[1]
+            _req(M % toks == 0, "rows must be whole samples of the freq table's tokens")
+            a.norm_freq, a.norm_freq_batch, a.norm_tokens = norm_freq.data_ptr(), norm_freq.shape[0], toks
+            a.norm_head_dim = norm_head_dim
     if epilogue in (EPI_BIAS_GATE_RES, EPI_BIAS_RES):
         _req(residual is not None, "residual required")
         r2 = residual.reshape(-1, N)
@@ -179,7 +209,10 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
     _lib.check(_lib.lib().wam_linear(ctypes.byref(a), stream_handle(dev)), "wam_linear")
     if scratch is not None:
         scratch.record_stream(torch.cuda.current_stream(dev))
-    return outs[0] if single else outs
+    res = outs[0] if single else outs
+    if ssqs is not None:
+        return res, (ssqs[0] if single else ssqs)
+    return res
 
 
 def ln_modulate(x, table, temb, shift_index, eps=1e-6, out=None):
@@ -242,12 +275,15 @@ def rms_rope(tensors, gammas, eps, freq=None, head_dim=128, out=None):
 
 
 def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, pool_rows=None,
-              kv_rows=None, scale=None, out=None):
+              kv_rows=None, scale=None, out=None, q_ssq=None, q_eps=1e-6):
     """softmax(q [history || k]^T / sqrt(hd)) [history || v] per head.
 
     q [B, Mq, H, 128]; k, v [Bk, Mk, H, 128] (any row stride, unit last dim);
     history = pool_k/pool_v [Bp, P, H, 128] at slots[:n_hist] (int32, device),
-    pool row pool_rows[b] (int64) or b; own row kv_rows[b] or b."""
+    pool row pool_rows[b] (int64) or b; own row kv_rows[b] or b.
+    q_ssq: fp32 [B * Mq, n] partial sums of squares of each query row (the
+    norm epilogue of linear); query rows are then scaled by
+    rsqrt(sum / (H * 128) + q_eps) (RMSNorm across heads)."""
     dev = _dev(q, k, v, pool_k, pool_v, slots, n_hist, pool_rows, kv_rows)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _bf16(t, n)
@@ -278,6 +314,10 @@ def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, poo
         _req(kv_rows.dtype == torch.int64 and kv_rows.numel() == B, "kv_rows int64 [B]")
         a.kv_rows = kv_rows.data_ptr()
     a.scale = scale if scale is not None else 1.0 / math.sqrt(hd)
+    if q_ssq is not None:
+        _req(q_ssq.dtype == torch.float32 and q_ssq.is_contiguous() and q_ssq.dim() == 2 and
+             q_ssq.shape[0] == B * Mq and q_ssq.device == dev, "q_ssq must be fp32 [B * Mq, n]")
+        a.q_ssq, a.q_ssq_n, a.q_norm_dim, a.q_eps = q_ssq.data_ptr(), q_ssq.shape[1], H * hd, q_eps
     # the key count bound plans the split: own keys plus the whole pool
     a.max_keys = a.Mk + (pool_k.shape[1] if n_hist is not None else 0)
     ws = None
