@@ -48,21 +48,21 @@ __device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n -
 // for query row b * Mq + qi (clamped into range).  The RMSNorm across heads
 // is model.py:609-612; the rotation after it is linear and commutes.
 constexpr int kQssqMax = 16;
-// The loads are unconditional (clamped index, then a select), so that no
-// branch separates them from the code after them.
+// The loads are unconditional (clamped index, no branch), and nothing is
+// computed from them here: the mask and the sum are in q_ssq_factor, so that
+// the wait for them falls where the factor is first needed (a branch or a
+// select here made the compiler wait for every load in flight, the first
+// K/V tiles included, before the first tile's barrier).
 __device__ inline void q_ssq_load(const wam_attention_args& a, int b, int qi, float qp[kQssqMax]) {
   const float* p = a.q_ssq + ((int64_t)b * a.Mq + min(qi, a.Mq - 1)) * a.q_ssq_n;
   const int last = a.q_ssq_n - 1;
 #pragma unroll
-  for (int t = 0; t < kQssqMax; ++t) {
-    const float v = p[min(t, last)];
-    qp[t] = t <= last ? v : 0.f;
-  }
+  for (int t = 0; t < kQssqMax; ++t) qp[t] = p[min(t, last)];
 }
 __device__ inline float q_ssq_factor(const wam_attention_args& a, const float qp[kQssqMax]) {
   float s = 0.f;
 #pragma unroll
-  for (int t = 0; t < kQssqMax; ++t) s += qp[t];
+  for (int t = 0; t < kQssqMax; ++t) s += t < a.q_ssq_n ? qp[t] : 0.f;
   return rsqrtf(s / (float)a.q_norm_dim + a.q_eps);
 }
 __device__ inline float q_rms_factor(const wam_attention_args& a, int b, int qi) {
@@ -408,8 +408,11 @@ template <bool HIST, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
                                                                   int n_full, int n_split, float* __restrict__ part) {
   static_assert(NW == 8 || (NW == 7 && !HIST), "8 waves, or 7 without pool keys");
-  // three K/V stages, then (pool keys only) the 64 slots of each stage's tile
-  __shared__ __attribute__((aligned(1024))) char lds[3 * kAttnStage + (HIST ? 3 * kAttnKT * 4 : 0)];
+  // three K/V stages, then (pool keys only) the 64 slots of each stage's
+  // tile, then each wave's query partial sums of squares (q_ssq)
+  constexpr int kQpSlots = kQssqMax / 2;  // direct-to-LDS dword loads per wave: 2 partials each
+  constexpr int kQpOff = 3 * kAttnStage + (HIST ? 3 * kAttnKT * 4 : 0);
+  __shared__ __attribute__((aligned(1024))) char lds[kQpOff + NW * kQpSlots * 256];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, half = lane >> 5;
@@ -523,8 +526,24 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   };
 
   // Softmax scale in log2 units; with q_ssq, times the query's 1/rms (set in
-  // the prologue, once the partial sums have had the first tile's time to land).
+  // the prologue).  The query's partial sums of squares go straight to LDS
+  // ahead of the first tile (slot i of a wave: partial 2 i in lanes 0-31 and
+  // 2 i + 1 in lanes 32-63), so the tile waits cover them and no register
+  // load wait is placed by the compiler; read back after the first barrier.
   float sc = a.scale * kLog2e;
+  char* const qp_lds = lds + kQpOff + wave * (kQpSlots * 256);
+  auto q_lds_load = [&]() {
+    const float* prow = a.q_ssq + ((int64_t)b * a.Mq + min(qi, a.Mq - 1)) * a.q_ssq_n;
+    const int slots_used = (a.q_ssq_n + 1) >> 1;
+    for (int i = 0; i < slots_used; ++i)
+      asm_g_ld4_lds((uint64_t)(uintptr_t)(prow + min(2 * i + half, a.q_ssq_n - 1)), qp_lds + i * 256);
+  };
+  auto q_lds_factor = [&]() {
+    float sum = 0.f;
+    for (int t = 0; t < a.q_ssq_n; ++t)
+      sum += *reinterpret_cast<const float*>(qp_lds + (t >> 1) * 256 + 4 * (l32 + 32 * (t & 1)));
+    return rsqrtf(sum / (float)a.q_norm_dim + a.q_eps);
+  };
   const int tr_i = lane & 15, tr_gh = (lane >> 4) & 1;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 o[4];
@@ -706,17 +725,18 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
+    if (a.q_ssq) q_lds_load();
     issue(t_first, 0);
     if (ntiles > 1) issue(t_first + 1, kAttnStage);
-    // (loaded after the tile loads: the wait for them then falls on the
-    // first step's own wait for tile 1)
-    float qp[kQssqMax];
-    if (a.q_ssq) q_ssq_load(a, b, qi, qp);
     if (ntiles > 1) wait_all_but_one_tile();
     else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     __builtin_amdgcn_s_barrier();
     s_mfma(0, s0);
-    if (a.q_ssq) sc *= q_ssq_factor(a, qp);
+    if (a.q_ssq) {
+      // the partials landed with tile 0 (issued before it); read after the barrier
+      asm volatile("" ::: "memory");
+      sc *= q_lds_factor();
+    }
     // Stages of tiles t, t+1 and t+2, rotated each step (scalar values; an
     // expression in t would become per-lane induction variables).
     int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;

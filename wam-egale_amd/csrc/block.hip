@@ -3,16 +3,15 @@
 //
 //   h1  = LN(x) * (1 + scale) + shift                       ln_modulate
 //   qkv = h1 [Wq|Wk|Wv]^T + b                               one GEMM launch
-//   q,k = rope(RMS(q) g_q), rope(RMS(k) g_k)                q: the GEMM's norm epilogue
-//                                                            (rope(y g_q) + sums of squares;
-//                                                            1/rms applied in attention),
-//                                                            k: rms_rope (in place)
+//   q,k = rope(RMS(q) g_q), rope(RMS(k) g_k)                rms_rope (in place)
 //   [pool bookkeeping]                                       kv_layout
 //   a1  = attention(q, [history || k], [history || v])       attention
 //   x1  = x + (a1 Wo^T + bo) * gate                          GEMM + gated residual
 //   [commit new K/V to the pool, update 1/2]                 kv_commit
 //   n2  = LN(x1) g2 + b2                                     ln_modulate (affine)
 //   cq  = RMS(n2 Wq2^T + bq2) g                              GEMM + norm epilogue
+//                                                            (y g + sums of squares;
+//                                                            1/rms applied in attention)
 //   ck, cv from context (or precomputed by prepare_context)  GEMM + rms_rope
 //   x2  = x1 + (attention(cq, ck, cv) Wo2^T + bo2)           attention + GEMM + residual
 //   h3  = LN(x2) * (1 + c_scale) + c_shift                   ln_modulate
@@ -92,8 +91,8 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   L.slots = take((size_t)(pool > 0 ? pool : 1) * 4);
   L.newslots = take((size_t)(M > 0 ? M : 1) * 4);
   L.info = take(16);
-  // Per-row sums of squares of the queries per 256-column group (the q-norm
-  // epilogue of the projection; self, then cross attention).
+  // Per-row sums of squares of the cross queries per 256-column group (the
+  // q-norm epilogue of the projection).
   L.ssq = take(R * (size_t)((D + 255) / 256) * 4);
   // Partial results of the self attention's key-range splits (own keys + the
   // pool), the cross attention's (context keys) and the split-K GEMM tails.
@@ -213,10 +212,12 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   int32_t* info = reinterpret_cast<int32_t*>(ws + L.info);
   float* qssq = reinterpret_cast<float*>(ws + L.ssq);
   const size_t rowb = (size_t)R * D * 2;
-  // Query norms: the projection's epilogue writes rope(y g) and the row's
-  // sums of squares, attention applies 1/rms.  With debug outputs requested
-  // the queries are normalised by the row pass instead, so that the debug
-  // copies hold the normalised tensors.
+  // Cross-attention query norm: the projection's epilogue writes y g and the
+  // row's sums of squares, attention applies 1/rms (no row pass).  With debug
+  // outputs requested the queries are normalised by the row pass instead, so
+  // that the debug copy holds the normalised tensor.  (For the self-attention
+  // queries the same fusion measured even: the QKV epilogue's cost matched
+  // the half of the q/k row pass it removes.)
   const bool qnorm_fused = a->debug == nullptr;
   const int qparts = (D + 255) / 256;
 
@@ -242,20 +243,15 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.w[1] = W->w[5]; g.bias[1] = W->w[6]; g.out[1] = qkv + D;
     g.w[2] = W->w[7]; g.bias[2] = W->w[8]; g.out[2] = qkv + 2 * D;
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
-    if (qnorm_fused) {
-      g.norm_ssq[0] = qssq; g.norm_gamma[0] = W->w[11];
-      g.norm_freq = a->freq; g.norm_freq_batch = a->freq_batch; g.norm_tokens = M;
-      g.norm_head_dim = W->head_dim;
-    }
     WAM_TRY(linear(&g, s));
   }
-  // 3. k (and, unfused, q) RMSNorm across heads + RoPE, in place.
+  // 3. q/k RMSNorm across heads + RoPE, in place.
   {
     Scope sc(a->timer, WAM_STAGE_RMS_ROPE, s);
     wam_rms_rope_args r{};
-    r.x[0] = qkv + D; r.y[0] = qkv + D; r.gamma[0] = W->w[12]; r.eps[0] = W->eps[4];
-    r.x[1] = qkv; r.y[1] = qkv; r.gamma[1] = W->w[11]; r.eps[1] = W->eps[3];
-    r.ldx = 3 * D; r.ldy = 3 * D; r.n_tensors = qnorm_fused ? 1 : 2; r.rows = R; r.D = D;
+    r.x[0] = qkv; r.y[0] = qkv; r.gamma[0] = W->w[11]; r.eps[0] = W->eps[3];
+    r.x[1] = qkv + D; r.y[1] = qkv + D; r.gamma[1] = W->w[12]; r.eps[1] = W->eps[4];
+    r.ldx = 3 * D; r.ldy = 3 * D; r.n_tensors = 2; r.rows = R; r.D = D;
     r.head_dim = W->head_dim;
     r.freq = a->freq; r.freq_batch = a->freq_batch; r.tokens = M;
     WAM_TRY(rms_rope(&r, s));
@@ -293,7 +289,6 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     t.max_keys = M + (cache ? a->pool : 0);
     t.scale = 1.0f / sqrtf((float)W->head_dim);
     t.workspace = L.split_bytes ? ws + L.split : nullptr; t.workspace_bytes = (int64_t)L.split_bytes;
-    if (qnorm_fused) { t.q_ssq = qssq; t.q_ssq_n = qparts; t.q_norm_dim = D; t.q_eps = W->eps[3]; }
     WAM_TRY(attention(&t, s));
   }
   WAM_TRY(copy_debug(a->debug, 4, attn, rowb, s));
