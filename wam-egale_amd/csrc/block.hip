@@ -34,6 +34,7 @@ int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
 int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys);
 int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K);
+bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes);
 int kv_layout(const wam_kv_layout_args*, hipStream_t);
 int kv_commit(const wam_kv_commit_args*, hipStream_t);
 
@@ -213,12 +214,14 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   float* qssq = reinterpret_cast<float*>(ws + L.ssq);
   const size_t rowb = (size_t)R * D * 2;
   // Cross-attention query norm: the projection's epilogue writes y g and the
-  // row's sums of squares, attention applies 1/rms (no row pass).  With debug
-  // outputs requested the queries are normalised by the row pass instead, so
-  // that the debug copy holds the normalised tensor.  (For the self-attention
-  // queries the same fusion measured even: the QKV epilogue's cost matched
-  // the half of the q/k row pass it removes.)
-  const bool qnorm_fused = a->debug == nullptr;
+  // row's sums of squares, attention applies 1/rms (no row pass), when the
+  // projection runs as one four-wave launch; other tilings would run the
+  // norm as a pass anyway, and the row pass is as fast.  With debug outputs
+  // requested the queries are normalised by the row pass, so that the debug
+  // copy holds the normalised tensor.  (For the self-attention queries the
+  // same fusion measured even: the QKV epilogue's cost matched the half of
+  // the q/k row pass it removes.)
+  const bool qnorm_fused = a->debug == nullptr && linear_norm_in_epilogue(R, D, 1, D, split_bytes);
   const int qparts = (D + 255) / 256;
 
   wam_modulation mod = a->mod;

@@ -1263,6 +1263,16 @@ int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K) {
   return plan_workspace(gemm_plan(M, seg_n, n_seg, K, device_cu_count(), INT64_MAX), M, seg_n);
 }
 
+// Whether linear() applies the q/k-norm epilogue inside a single four-wave
+// launch for this bf16 shape (otherwise it runs the GEMM and then the norm
+// pass, which costs about what a separate RMSNorm pass costs).
+bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes) {
+  if (M < 1 || K % 64 != 0 || !uses_big_tiles(M, seg_n, n_seg)) return false;
+  const int cus = device_cu_count();
+  if (w4_t224_wins(M, seg_n, n_seg, K, cus, ws_bytes)) return true;
+  return gemm_plan(M, seg_n, n_seg, K, cus, ws_bytes).kind == 0;
+}
+
 int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a != nullptr, "wam_linear: null args");
   WAM_REQUIRE(a->n_seg >= 1 && a->n_seg <= 3, "wam_linear: n_seg must be 1..3 (got %d)", a->n_seg);
