@@ -293,14 +293,25 @@ typedef struct {
   const float* ffn_scale[2];
 } wam_block_weights;
 
-#define WAM_DEBUG_SLOTS 16
+#define WAM_DEBUG_SLOTS 28
 /* debug[i] (if non-NULL) receives a copy of intermediate i:
  *  0 modulated1 [R,D]  1 self_q_rope [R,D]  2 self_k_rope [R,D]  3 self_v [R,D]
  *  4 self_attention [R,D]  5 residual1 [R,D] f32  6 norm2 [R,D]  7 cross_q [R,D]
  *  8 cross_k [Bc*Lc,D]  9 cross_v [Bc*Lc,D]  10 cross_attention [R,D]
  *  11 residual2 [R,D] f32  12 modulated3 [R,D]  13 gelu [R,F]  14 output [R,D]
- * (all bf16 except the two residual-stream tensors, which the block keeps in
- * fp32 between the input and the output) */
+ *  15 self_q_linear [R,D]  16 self_k_linear [R,D]  17 self_q_norm [R,D]
+ *  18 self_k_norm [R,D] (RMSNorm before RoPE)  19 self_out [R,D] (to_out before
+ *  the gate)  20 cross_q_linear [R,D]  21 cross_k_linear [Bc*Lc,D] (only when
+ *  the call projects the context; untouched with precomputed cross K/V)
+ *  22 cross_out [R,D]  23 ffn1 [R,F] (before GELU)  24 ffn2 [R,D] (before the
+ *  gate)  25 norm1 [R,D]  26 norm3 [R,D] (LayerNorm before the modulation)
+ *  27 modulation [B,L,6,D] f32 (table + temb)
+ * (all bf16 except the residual-stream tensors, which the block keeps in
+ * fp32 between the input and the output, and the modulation).  Slots 15-27
+ * are the reference's remaining named intermediates
+ * (optimized/csrc/whole_layer.cu:1203-1209); the fused kernels do not
+ * materialise them, so the block computes them with extra launches when
+ * they are requested. */
 
 typedef struct {
   const wam_block_weights* weights;

@@ -49,19 +49,34 @@ def _params(p, dtype):
 
 
 def attention(P, prefix, q_in, kv_in, rotary_emb, heads, eps_q, eps_k, cache=None,
-              update_cache=0, candidate_rows=None, evict_order="stable"):
-    """WanAttention.forward (model.py:595-691), original cache mode."""
+              update_cache=0, candidate_rows=None, evict_order="stable", keep=None, name=None):
+    """WanAttention.forward (model.py:595-691), original cache mode.  With `keep`,
+    records the intermediates `{name}_q_linear`, `_k_linear`, `_v`, `_q_norm`,
+    `_k_norm`, `_q_rope` and `_k_rope` (or `_q` and `_k` without RoPE),
+    `_attention`, `_out` (the reference's
+    debug names, optimized/csrc/whole_layer.cu:1203-1209)."""
     g = lambda n: P[f"{prefix}.{n}"]
+    rec = (lambda n, t: keep.__setitem__(f"{name}_{n}", t)) if keep is not None else (lambda n, t: None)
     D = q_in.shape[-1]
     q = F.linear(q_in, g("to_q.weight"), g("to_q.bias"))
     k = F.linear(kv_in, g("to_k.weight"), g("to_k.bias"))
     v = F.linear(kv_in, g("to_v.weight"), g("to_v.bias"))
+    rec("q_linear", q)
+    rec("k_linear", k)
+    rec("v", v)
     q = F.rms_norm(q, (D,), g("norm_q.weight"), eps_q).unflatten(2, (heads, -1))
     k = F.rms_norm(k, (D,), g("norm_k.weight"), eps_k).unflatten(2, (heads, -1))
+    rec("q_norm", q)
+    rec("k_norm", k)
     v = v.unflatten(2, (heads, -1))
     if rotary_emb is not None:
         q = apply_rope(q, rotary_emb)
         k = apply_rope(k, rotary_emb)
+        rec("q_rope", q)
+        rec("k_rope", k)
+    else:
+        rec("q", q)  # the reference names the unrotated (cross) q/k `cross_q`, `cross_k`
+        rec("k", k)
     if candidate_rows is not None:
         if update_cache != 0 or cache is None:
             raise ValueError("candidate verification requires existing read-only KV")
@@ -85,7 +100,10 @@ def attention(P, prefix, q_in, kv_in, rotary_emb, heads, eps_q, eps_k, cache=Non
         if update_cache == 0 and cache is not None:
             kvcache.restore_cache(cache, slots)
     out = out.flatten(2, 3).type_as(q)
-    return F.linear(out, g("to_out.0.weight"), g("to_out.0.bias"))
+    rec("attention", out)
+    out = F.linear(out, g("to_out.0.weight"), g("to_out.0.bias"))
+    rec("out", out)
+    return out
 
 
 def block_forward(params, x, context, temb, rotary_emb, heads, eps=1e-6, cache=None,
@@ -101,11 +119,14 @@ def block_forward(params, x, context, temb, rotary_emb, heads, eps=1e-6, cache=N
     D = x.shape[-1]
     keep = intermediates if intermediates is not None else {}
     mod = P["scale_shift_table"][None] + temb.float()
+    keep["modulation"] = mod
     shift, scale, gate, c_shift, c_scale, c_gate = (mod[:, :, i] for i in range(6))
-    h = (F.layer_norm(x.float(), (D,), eps=eps7[0]) * (1.0 + scale) + shift).to(dtype)
+    n1 = F.layer_norm(x.float(), (D,), eps=eps7[0])
+    keep["norm1"] = n1
+    h = (n1 * (1.0 + scale) + shift).to(dtype)
     keep["modulated1"] = h
     a = attention(P, "attn1", h, h, rotary_emb, heads, eps7[3], eps7[4], cache, update_cache,
-                  candidate_rows, evict_order)
+                  candidate_rows, evict_order, keep=keep, name="self")
     x = (x.float() + a * gate).to(dtype)
     keep["residual1"] = x
     if "norm2.weight" in P:
@@ -113,15 +134,19 @@ def block_forward(params, x, context, temb, rotary_emb, heads, eps=1e-6, cache=N
     else:
         n2 = x
     keep["norm2"] = n2
-    a = attention(P, "attn2", n2, context, None, heads, eps7[5], eps7[6])
+    a = attention(P, "attn2", n2, context, None, heads, eps7[5], eps7[6], keep=keep, name="cross")
     x = x + a
     keep["residual2"] = x
-    h = (F.layer_norm(x.float(), (D,), eps=eps7[2]) * (1.0 + c_scale) + c_shift).to(dtype)
+    n3 = F.layer_norm(x.float(), (D,), eps=eps7[2])
+    keep["norm3"] = n3
+    h = (n3 * (1.0 + c_scale) + c_shift).to(dtype)
     keep["modulated3"] = h
     f = F.linear(h, P["ffn.net.0.proj.weight"], P["ffn.net.0.proj.bias"])
+    keep["ffn1"] = f
     f = F.gelu(f, approximate="tanh")
     keep["gelu"] = f
     f = F.linear(f, P["ffn.net.2.weight"], P["ffn.net.2.bias"])
+    keep["ffn2"] = f
     out = (x.float() + f.float() * c_gate).to(dtype)
     keep["output"] = out
     return out

@@ -94,7 +94,8 @@ def test_workspace_size():
     n = h.wam_block_workspace_bytes(1, R, D, F, 1, Lc, 0)
     expect = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
               + R * 4  # new-slot list
-              + R * (D // 256) * 4)  # per-row query sums of squares per 256-column group
+              + R * (D // 256) * 4  # per-row query sums of squares per 256-column group
+              + (1 + 2) * D * 4)  # zero modulation for the unmodulated LayerNorm debug outputs
     assert expect <= n < expect + 4096
     # 4680 queries over their own 4680 keys fill two dispatch rounds: no split
     assert h.wam_attention_workspace_bytes(1, R, 24, R) == 0
@@ -131,7 +132,8 @@ def test_attention_split_plan_workspace():
     R = B * M
     core = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
             + P * 4 + M * 4  # slot lists
-            + R * (D // 256) * 4)  # query sums of squares
+            + R * (D // 256) * 4  # query sums of squares
+            + (B + 2) * D * 4)  # zero modulation (debug LayerNorms)
     need = max(h.wam_attention_workspace_bytes(B, M, 24, M + P), h.wam_linear_workspace_bytes(R, D, 1, F),
                h.wam_linear_workspace_bytes(R, F, 1, D))
     assert need > 0

@@ -73,7 +73,7 @@ struct Scope {
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct Layout {
-  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, ssq, split, split_bytes, total;
+  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, ssq, zeros, split, split_bytes, total;
 };
 
 static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
@@ -95,6 +95,9 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   // Per-row sums of squares of the cross queries per 256-column group (the
   // q-norm epilogue of the projection).
   L.ssq = take(R * (size_t)((D + 255) / 256) * 4);
+  // A zero modulation (table [2, D] and one vector per batch row) for the
+  // unmodulated LayerNorm debug outputs.
+  L.zeros = take(((size_t)B + 2) * D * 4);
   // Partial results of the self attention's key-range splits (own keys + the
   // pool), the cross attention's (context keys) and the split-K GEMM tails.
   // One region: the kernels that use it run one after another on the stream.
@@ -122,6 +125,24 @@ static int cast_f32_bf16(const float* x, bf16* y, int64_t n, hipStream_t s) {
                      0, s, x, y, n);
   WAM_LAUNCHED("cast_f32_bf16_kernel");
   return WAM_OK;
+}
+
+__global__ void fill_zero_kernel(float* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
+}
+
+// modulation[b, l, i, d] = table[i, d] + temb[b, l, i, d] in fp32 (the
+// reference's `modulation` intermediate, model.py:751-759).
+__global__ void modulation_table_kernel(wam_modulation m, int D, int64_t n, float* out) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int d = (int)(e % D);
+    const int i = (int)((e / D) % 6);
+    const float t = m.table_dtype == WAM_F32 ? static_cast<const float*>(m.table)[i * D + d]
+                                             : static_cast<float>(static_cast<const bf16*>(m.table)[i * D + d]);
+    const float u = m.temb_dtype == WAM_F32 ? static_cast<const float*>(m.temb)[e]
+                                            : static_cast<float>(static_cast<const bf16*>(m.temb)[e]);
+    out[e] = t + u;
+  }
 }
 
 static int copy_debug(void** dbg, int slot, const void* src, size_t bytes, hipStream_t s) {
@@ -156,12 +177,14 @@ static void gemm_args(wam_linear_args& g, const void* a, int64_t lda, int M, int
 
 // Cross K/V of the context rows: k = RMS(ctx Wk^T + bk) g, v = ctx Wv^T + bv.
 static int context_kv(const wam_block_weights* W, const void* ctx, int rows, void* k, void* v,
-                      hipStream_t s) {
+                      hipStream_t s, void* k_linear_debug = nullptr) {
   const int D = W->dim;
   wam_linear_args g;
   gemm_args(g, ctx, D, rows, D, D, W->w[15], W->w[16], k, D);
   g.n_seg = 2; g.w[1] = W->w[17]; g.bias[1] = W->w[18]; g.out[1] = v;
   WAM_TRY(linear(&g, s));
+  if (k_linear_debug)
+    WAM_HIP(hipMemcpyAsync(k_linear_debug, k, (size_t)rows * D * 2, hipMemcpyDeviceToDevice, s));
   wam_rms_rope_args r{};
   r.x[0] = k; r.y[0] = k; r.gamma[0] = W->w[22]; r.eps[0] = W->eps[6];
   r.ldx = D; r.ldy = D; r.n_tensors = 1; r.rows = rows; r.D = D; r.head_dim = W->head_dim;
@@ -237,6 +260,40 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     WAM_TRY(ln_modulate(&l, s));
   }
   WAM_TRY(copy_debug(a->debug, 0, h, rowb, s));
+  // Debug only: the reference's unfused intermediates (slots 15-27), each
+  // by an extra launch where the fused kernels do not materialise it.
+  auto dbg = [&](int i) -> void* { return a->debug ? a->debug[i] : nullptr; };
+  float* zeros = reinterpret_cast<float*>(ws + L.zeros);
+  auto plain_ln = [&](const void* x, int x_dtype, float eps, void* y) -> int {
+    // LayerNorm without modulation: a zero table [2, D] and zero vectors
+    wam_ln_args l{};
+    l.x = x; l.x_dtype = x_dtype; l.y = y; l.rows = R; l.D = D; l.eps = eps; l.affine = 0;
+    l.mod.table = zeros; l.mod.table_dtype = WAM_F32; l.mod.temb = zeros + 2 * D; l.mod.temb_dtype = WAM_F32;
+    l.mod.temb_len = 1; l.mod.tokens = M; l.mod.temb_mods = 1; l.shift_index = 0;
+    return ln_modulate(&l, s);
+  };
+  auto plain_linear = [&](const void* x, int K, int N, int wi, int wf8, void* y) -> int {
+    // bias epilogue only, with the same weights as the fused launch
+    wam_linear_args g;
+    gemm_args(g, x, K, R, K, N, W->w[wi], W->w[wi + 1], y, N);
+    if (wf8 >= 0 && W->ffn_fp8[0]) {
+      g.w[0] = W->ffn_fp8[wf8]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[wf8];
+    }
+    g.workspace = split_ws; g.workspace_bytes = split_bytes;
+    return linear(&g, s);
+  };
+  if (dbg(25) || dbg(26)) {
+    const int64_t nz = ((int64_t)B + 2) * D;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((nz + 255) / 256)), dim3(256), 0, s, zeros, nz);
+    WAM_LAUNCHED("fill_zero_kernel");
+  }
+  if (dbg(25)) WAM_TRY(plain_ln(a->x, WAM_BF16, W->eps[0], dbg(25)));
+  if (dbg(27)) {
+    const int64_t n = (int64_t)B * mod.temb_len * 6 * D;
+    hipLaunchKernelGGL(modulation_table_kernel, dim3((unsigned)((n + 255) / 256 < 16384 ? (n + 255) / 256 : 16384)),
+                       dim3(256), 0, s, mod, D, n, static_cast<float*>(dbg(27)));
+    WAM_LAUNCHED("modulation_table_kernel");
+  }
   // 2. Q|K|V projection as one launch into the packed [R, 3D] buffer.
   {
     Scope sc(a->timer, WAM_STAGE_QKV, s);
@@ -247,6 +304,16 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.w[2] = W->w[7]; g.bias[2] = W->w[8]; g.out[2] = qkv + 2 * D;
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
+  }
+  for (int i = 0; i < 2; ++i) {
+    if (dbg(15 + i))
+      WAM_HIP(hipMemcpy2DAsync(dbg(15 + i), D * 2, qkv + i * D, 3 * D * 2, D * 2, R, hipMemcpyDeviceToDevice, s));
+    if (dbg(17 + i)) {
+      wam_rms_rope_args r{};
+      r.x[0] = qkv + i * D; r.y[0] = dbg(17 + i); r.gamma[0] = W->w[11 + i]; r.eps[0] = W->eps[3 + i];
+      r.ldx = 3 * D; r.ldy = D; r.n_tensors = 1; r.rows = R; r.D = D; r.head_dim = W->head_dim;
+      WAM_TRY(rms_rope(&r, s));
+    }
   }
   // 3. q/k RMSNorm across heads + RoPE, in place.
   {
@@ -316,6 +383,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 5, x1, rowb * 2, s));
+  if (dbg(19)) WAM_TRY(plain_linear(attn, D, D, 9, -1, dbg(19)));
   // 8. norm2 (affine LayerNorm), or without cross_attn_norm the bf16 cast
   //    of the residual stream that the identity norm2 passes through.
   const bf16* n2 = h;
@@ -340,6 +408,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     if (qnorm_fused) { g.norm_ssq[0] = qssq; g.norm_gamma[0] = W->w[21]; }
     WAM_TRY(linear(&g, s));
+    WAM_TRY(copy_debug(a->debug, 20, cq, rowb, s));
     if (!qnorm_fused) {
       wam_rms_rope_args r{};
       r.x[0] = cq; r.y[0] = cq; r.gamma[0] = W->w[21]; r.eps[0] = W->eps[5];
@@ -354,7 +423,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   const size_t ctxb = (size_t)a->context_batch * a->context_len * D * 2;
   if (!precomputed) {
     Scope sc(a->timer, WAM_STAGE_CROSS_KV, s);
-    WAM_TRY(context_kv(W, a->context, a->context_batch * a->context_len, ws + L.ck, ws + L.cv, s));
+    WAM_TRY(context_kv(W, a->context, a->context_batch * a->context_len, ws + L.ck, ws + L.cv, s, dbg(21)));
     ck = ws + L.ck;
     cv = ws + L.cv;
   }
@@ -388,6 +457,8 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 11, x2, rowb * 2, s));
+  if (dbg(22)) WAM_TRY(plain_linear(attn, D, D, 19, -1, dbg(22)));
+  if (dbg(26)) WAM_TRY(plain_ln(x2, WAM_F32, W->eps[2], dbg(26)));
   // 13. LN3 + modulation (c_shift 3, c_scale 4).
   {
     Scope sc(a->timer, WAM_STAGE_LN3, s);
@@ -397,6 +468,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     WAM_TRY(ln_modulate(&l, s));
   }
   WAM_TRY(copy_debug(a->debug, 12, h, rowb, s));
+  if (dbg(23)) WAM_TRY(plain_linear(h, D, F, 23, 0, dbg(23)));
   // 14. FFN1 + GELU(tanh).
   {
     Scope sc(a->timer, WAM_STAGE_FFN1, s);
@@ -410,6 +482,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     WAM_TRY(linear(&g, s));
   }
   WAM_TRY(copy_debug(a->debug, 13, act, (size_t)R * F * 2, s));
+  if (dbg(24)) WAM_TRY(plain_linear(act, F, D, 25, 1, dbg(24)));
   // 15. FFN2 + gated residual (c_gate 5).
   {
     Scope sc(a->timer, WAM_STAGE_FFN2, s);

@@ -19,13 +19,16 @@ WAM_BF16, WAM_F32, WAM_FP8, WAM_I64, WAM_F64 = 0, 1, 2, 3, 4
 WAM_ACT_NONE, WAM_ACT_SILU = 0, 1
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATE_RES, EPI_BIAS_RES = 0, 1, 2, 3
 PEAK_BF16_32, PEAK_BF16_16, PEAK_FP8_32, PEAK_FP8_16 = 0, 1, 2, 3
-DEBUG_SLOTS = 16
+DEBUG_SLOTS = 28
 STAGES = ("ln1", "qkv", "rms_rope", "kv_layout", "self_attn", "self_out", "ln2",
           "cross_q", "cross_kv", "cross_attn", "cross_out", "ln3", "ffn1", "ffn2",
           "kv_commit")
 DEBUG_NAMES = ("modulated1", "self_q_rope", "self_k_rope", "self_v", "self_attention",
                "residual1", "norm2", "cross_q", "cross_k", "cross_v", "cross_attention",
-               "residual2", "modulated3", "gelu", "output")
+               "residual2", "modulated3", "gelu", "output",
+               "self_q_linear", "self_k_linear", "self_q_norm", "self_k_norm", "self_out",
+               "cross_q_linear", "cross_k_linear", "cross_out", "ffn1", "ffn2", "norm1", "norm3",
+               "modulation")
 
 
 class Modulation(Structure):

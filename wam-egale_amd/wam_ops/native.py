@@ -199,13 +199,19 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     if debug:
         R = B * M
         Lc = ctx.shape[0] * ctx.shape[1]
-        shapes = [(R, D)] * 8 + [(Lc, D), (Lc, D)] + [(R, D)] * 3 + [(R, bound.ffn_dim), (R, D)]
-        fp32 = ("residual1", "residual2")  # the block's residual stream is fp32
+        F = bound.ffn_dim
+        shapes = ([(R, D)] * 8 + [(Lc, D), (Lc, D)] + [(R, D)] * 3 + [(R, F), (R, D)]
+                  + [(R, D)] * 5 + [(R, D), (Lc, D), (R, D), (R, F)] + [(R, D)] * 3
+                  + [(temb.shape[0], temb.shape[1], 6, D)])
+        # the block's residual stream is fp32, and so is the modulation table
+        fp32 = ("residual1", "residual2", "modulation")
         dbg = {n: torch.empty(s, dtype=torch.float32 if n in fp32 else torch.bfloat16, device=dev)
                for n, s in zip(_lib.DEBUG_NAMES, shapes)}
+        if cross_kv is not None:
+            del dbg["cross_k_linear"]  # the context is not projected in this call
         arr = (ctypes.c_void_p * _lib.DEBUG_SLOTS)()
         for i, n in enumerate(_lib.DEBUG_NAMES):
-            arr[i] = dbg[n].data_ptr()
+            arr[i] = dbg[n].data_ptr() if n in dbg else None
         args.debug = ctypes.cast(arr, ctypes.c_void_p)
     if timer is not None:
         args.timer = timer
