@@ -165,9 +165,12 @@ def test_rms_rope(dev, B, M, H):
 # sums of squares and bf16(rope(y * gamma)) have exact references.  4680
 # rows end in the four-wave kernel (224-row tiles; three segments = QKV, one
 # = cross q); 520 and 120 rows in other tile kernels plus the norm pass; 6240
-# rows = 4 samples of 1560 tokens sharing one RoPE table (row modulo tokens).
+# rows = 4 samples of 1560 tokens sharing one RoPE table (row modulo tokens,
+# one wrap per row); 4680 rows of 26 samples of 180 tokens (a modulo per row);
+# 5120 rows, one segment: 256-row tiles in one round.
 @pytest.mark.parametrize("M,nseg,grid", [(4680, 3, (6, 26, 30)), (4680, 1, None), (520, 3, (2, 10, 26)),
-                                         (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30))])
+                                         (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30)),
+                                         (4680, 3, (1, 12, 15)), (5120, 1, (5, 32, 32))])
 def test_linear_qk_norm(dev, M, nseg, grid):
     from wam_ops import ops, synthetic
     K = N = 3072
