@@ -713,6 +713,44 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
     }
   };
 
+  // A wave whose 32 queries all lie past Mq (in the partial last query tile
+  // of a row: 1560 = 6 x 256 + 24 leaves seven of its eight waves without
+  // queries) computes nothing: it issues its share of every tile's loads and
+  // the slot lists, and joins every barrier of the schedule below (one after
+  // the slot lists, one in the prologue, one per step), then exits.
+  const bool live = qt * QT + wave * 32 < a.Mq;  // wave-uniform
+  if (!live) {
+    if (ntiles > 0) {
+      if (HIST) {
+        load_slots(t_first, 0);
+        if (ntiles > 1) load_slots(t_first + 1, kAttnStage);
+        if (ntiles > 2) load_slots(t_first + 2, 2 * kAttnStage);
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      }
+      issue(t_first, 0);
+      if (ntiles > 1) issue(t_first + 1, kAttnStage);
+      if (ntiles > 1) wait_all_but_one_tile();
+      else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      __builtin_amdgcn_s_barrier();
+      int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
+      for (int t = 0; t < ntiles; ++t) {
+        const int T = t_first + t;
+        if (t + 1 < ntiles) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        __builtin_amdgcn_s_barrier();
+        if (HIST) asm volatile("" ::: "memory");
+        if (t + 2 < ntiles) issue(T + 2, st2);
+        if (t + 3 < ntiles) load_slots(T + 3, st0);
+        const int st_done = st0;
+        st0 = st1;
+        st1 = st2;
+        st2 = st_done;
+      }
+    }
+    return;
+  }
+
   if (ntiles > 0) {
     // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
     // tile 0 has landed.
