@@ -46,29 +46,14 @@ __device__ inline int clamp_row(int r, int n) { return r < 0 ? 0 : (r >= n ? n -
 // Per-query RMS factor of queries written by wam_linear's norm epilogue:
 // rsqrt(sum of the row's q_ssq_n partial sums of squares / q_norm_dim + eps)
 // for query row b * Mq + qi (clamped into range).  The RMSNorm across heads
-// is model.py:609-612; the rotation after it is linear and commutes.
+// is model.py:609-612; the rotation after it is linear and commutes.  The
+// pipelined kernel stages the partial sums through LDS instead (see there).
 constexpr int kQssqMax = 16;
-// The loads are unconditional (clamped index, no branch), and nothing is
-// computed from them here: the mask and the sum are in q_ssq_factor, so that
-// the wait for them falls where the factor is first needed (a branch or a
-// select here made the compiler wait for every load in flight, the first
-// K/V tiles included, before the first tile's barrier).
-__device__ inline void q_ssq_load(const wam_attention_args& a, int b, int qi, float qp[kQssqMax]) {
-  const float* p = a.q_ssq + ((int64_t)b * a.Mq + min(qi, a.Mq - 1)) * a.q_ssq_n;
-  const int last = a.q_ssq_n - 1;
-#pragma unroll
-  for (int t = 0; t < kQssqMax; ++t) qp[t] = p[min(t, last)];
-}
-__device__ inline float q_ssq_factor(const wam_attention_args& a, const float qp[kQssqMax]) {
-  float s = 0.f;
-#pragma unroll
-  for (int t = 0; t < kQssqMax; ++t) s += t < a.q_ssq_n ? qp[t] : 0.f;
-  return rsqrtf(s / (float)a.q_norm_dim + a.q_eps);
-}
 __device__ inline float q_rms_factor(const wam_attention_args& a, int b, int qi) {
-  float qp[kQssqMax];
-  q_ssq_load(a, b, qi, qp);
-  return q_ssq_factor(a, qp);
+  const float* p = a.q_ssq + ((int64_t)b * a.Mq + min(qi, a.Mq - 1)) * a.q_ssq_n;
+  float s = 0.f;
+  for (int t = 0; t < a.q_ssq_n; ++t) s += p[t];
+  return rsqrtf(s / (float)a.q_norm_dim + a.q_eps);
 }
 
 // Workgroup: W waves x 32 queries of one (batch row, head).  Wave w owns
