@@ -53,6 +53,37 @@ def test_linear_host_validation():
     assert "residual" in _err(h.wam_linear(ctypes.byref(a), None))
 
 
+
+def test_norm_epilogue_host_validation():
+    """The q/k-norm epilogue of wam_linear and the query RMS factor of
+    wam_attention reject bad arguments before any launch."""
+    h = _lib.lib()
+    a = _lib.LinearArgs()
+    a.a, a.lda, a.M, a.K, a.n_seg, a.seg_n, a.ldw, a.ldo = 16, 128, 8, 128, 1, 128, 128, 128
+    a.w[0], a.out[0] = 16, 16
+    a.norm_ssq[0] = 16
+    a.epilogue = _lib.EPI_BIAS_GELU
+    assert "needs WAM_EPI_BIAS" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.epilogue = _lib.EPI_BIAS
+    assert "needs a gamma" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.norm_gamma[0] = 16
+    a.norm_ssq[1] = 16  # a segment that the launch does not have
+    assert "norm segment 1" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.norm_ssq[1] = None
+    a.norm_freq, a.norm_head_dim, a.norm_tokens, a.norm_freq_batch = 16, 96, 8, 1
+    assert "head_dim 96" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.norm_head_dim, a.norm_tokens = 128, 3
+    assert "freq batch" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.norm_tokens, a.norm_freq = 8, 24
+    assert "16-byte aligned" in _err(h.wam_linear(ctypes.byref(a), None))
+    t = _lib.AttentionArgs()
+    t.B, t.Mq, t.H, t.head_dim, t.Mk, t.kv_batch = 1, 4, 1, 128, 4, 1
+    t.q = t.o = t.k = t.v = 16
+    t.q_ssq, t.q_ssq_n, t.q_norm_dim = 16, 17, 128
+    assert "q_ssq needs 1..16 partials" in _err(h.wam_attention(ctypes.byref(t), None))
+    t.q_ssq_n, t.q_norm_dim = 1, 0
+    assert "q_norm_dim" in _err(h.wam_attention(ctypes.byref(t), None))
+
 def test_attention_host_validation():
     h = _lib.lib()
     a = _lib.AttentionArgs()
