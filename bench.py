@@ -440,6 +440,9 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "FFN1 GEMM 4680x14336x3072 + bias + GELU(tanh)",
                      "achieved": round(ffn1_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ffn1_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
+                     "traffic_source": ("profiles/" + TRAFFIC_FILE.name + " (rocprofv3 FETCH_SIZE and "
+                                        "WRITE_SIZE passes over bench.py --pmc-ffn1; not measured in "
+                                        "this run)"),
                      "kernel_us": round(ffn1 * 1e3, 1),
                      "peak_measured": peak_meas,
                      "frac_of_measured": round(ffn1_tflops / peak_meas, 4)},

@@ -238,9 +238,12 @@ int64_t wam_attention_workspace_bytes(int B, int Mq, int H, int max_keys);
  * HIP graph capture, serving loops that forbid hipMalloc).  args->workspace
  * must be NULL and workspace_bytes 0; the key-range split's partial results
  * go to a static 64 MiB device array of the library (one per GPU, held until
- * the process ends).  A shape whose split needs more than that
- * (wam_attention_workspace_bytes > 64 MiB) is refused with WAM_ERR_ARG.
- * Calls that overlap on one GPU share the array and race. */
+ * the process ends).  A call whose own key-range split (the plan this call
+ * would run, with the query tile this call would use) needs more than 64 MiB
+ * of partials is refused with WAM_ERR_ARG.  wam_attention_workspace_bytes
+ * may report more than that plan needs (it covers every query tile), so it
+ * is an upper bound, not the test.  Calls that overlap on one GPU share the
+ * array and race. */
 int wam_attention_noalloc(const wam_attention_args* args, void* stream);
 
 /* ------------------------------------------------------------- KV pool */
@@ -330,10 +333,15 @@ typedef struct {
   int update;
   /* precomputed cross K/V [Bc, Lc, D] (already RMS-normed K); NULL = compute */
   const void* cross_k; const void* cross_v;
-  void* out;                    /* [B, M, D] bf16 */
+  void* out;                    /* [B, M, D] bf16 (or fp32, out_dtype) */
   void* workspace; size_t workspace_bytes;
   void** debug;                 /* NULL or WAM_DEBUG_SLOTS pointers */
   void* timer;                  /* NULL or a wam_timer */
+  /* WAM_BF16 (0, the reference's output) or WAM_F32: the final gated
+   * residual x2 + f * c_gate before its bf16 rounding, i.e. the block's
+   * arithmetic without the output's own rounding (a parity diagnostic; the
+   * reference block returns bf16). */
+  int out_dtype;
 } wam_block_args;
 
 size_t wam_block_workspace_bytes(int B, int M, int dim, int ffn_dim,

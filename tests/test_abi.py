@@ -51,6 +51,12 @@ def test_linear_host_validation():
     assert "n_seg" in _err(h.wam_linear(ctypes.byref(a), None))
     a.n_seg, a.epilogue = 1, _lib.EPI_BIAS_GATE_RES
     assert "residual" in _err(h.wam_linear(ctypes.byref(a), None))
+    # the epilogue addresses rows of one tile in 32 bits: strides of 2^21
+    # elements (8 MiB fp32 rows) and more are refused
+    a.epilogue, a.ldo = _lib.EPI_BIAS, 1 << 21
+    assert "2^21" in _err(h.wam_linear(ctypes.byref(a), None))
+    a.ldo, a.ldr = 128, 1 << 21
+    assert "2^21" in _err(h.wam_linear(ctypes.byref(a), None))
 
 
 

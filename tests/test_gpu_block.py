@@ -129,6 +129,38 @@ def test_block_debug_intermediates(dev):
         assert_close(got, ref, max_abs=bound, min_cos=0.9999, what=f"debug {name}")
 
 
+def test_block_debug_l4680_runs_the_same_kernels(dev):
+    """At L4680 the cross-attention queries are normalised in the projection's
+    epilogue and attention applies their 1/rms.  A debug call runs those same
+    kernels (the debug copies come from extra launches), so its output equals
+    a normal call's bit for bit; its cross-q intermediates (the projection
+    before the norm, the normalised queries) and the cross-attention output
+    match the oracle's."""
+    from wam_ops import synthetic
+    from wam_ops.native import NativeBlock
+    shape = synthetic.WAN22_5B
+    params = synthetic.block_params(shape, seed=11)
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4680, (6, 26, 30), context_len=512, seed=12)
+    inter = {}
+    block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps, intermediates=inter)
+    blk = native_block(params, shape, dev)
+    with torch.no_grad():
+        out = blk(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+        dbg = NativeBlock(blk)(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), debug=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dbg["output"], out), "a debug call changed the block output"
+    for name in ("cross_q_linear", "cross_q", "cross_attention", "output"):
+        ref = inter[name].float()
+        got = dbg[name].reshape(ref.shape).float().cpu()
+        # half an ulp of the largest value plus accumulation noise; the
+        # normalised queries are formed from the rounded projection (whose
+        # own error is that bound) and rounded again: two half-ulps
+        ulps = 2 if name == "cross_q" else 1
+        bound = max(2e-2, ulps * 2.0 ** -8 * ref.abs().max().item() + 2e-3)
+        m = assert_close(got, ref, max_abs=bound, min_cos=0.9999, what=f"L4680 debug {name}")
+        print(f"L4680 debug {name}: {m['max_abs']:.5f} (bound {bound:.4f})")
+
+
 def test_cache_protocol_sequence(dev):
     """update 2 -> 1 -> 0 -> candidate rows, outputs and pool state vs the oracle."""
     from wam_ops import synthetic

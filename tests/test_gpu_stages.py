@@ -167,10 +167,14 @@ def test_rms_rope(dev, B, M, H):
 # = cross q); 520 and 120 rows in other tile kernels plus the norm pass; 6240
 # rows = 4 samples of 1560 tokens sharing one RoPE table (row modulo tokens,
 # one wrap per row); 4680 rows of 26 samples of 180 tokens (a modulo per row);
-# 5120 rows, one segment: 256-row tiles in one round.
+# 5120 rows, one segment: 256-row tiles in one round.  "per-sample": a
+# [2, tokens, 1, 64] table whose two samples differ (row m reads table row m,
+# no modulo), on the fused four-wave path (4680 rows) and on the norm pass
+# (520 rows).
 @pytest.mark.parametrize("M,nseg,grid", [(4680, 3, (6, 26, 30)), (4680, 1, None), (520, 3, (2, 10, 26)),
                                          (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30)),
-                                         (4680, 3, (1, 12, 15)), (5120, 1, (5, 32, 32))])
+                                         (4680, 3, (1, 12, 15)), (5120, 1, (5, 32, 32)),
+                                         (4680, 1, "per-sample"), (520, 1, "per-sample")])
 def test_linear_qk_norm(dev, M, nseg, grid):
     from wam_ops import ops, synthetic
     K = N = 3072
@@ -179,7 +183,16 @@ def test_linear_qk_norm(dev, M, nseg, grid):
     ws = [_randn((N, K), dev, 10 + i, 0.02) for i in range(nseg)]
     bs = [_randn((N,), dev, 20 + i, 0.02) for i in range(nseg)]
     gs = [_randn((N,), dev, 30 + i, 0.1) + 1 for i in range(min(nseg, 2))] + [None] * (nseg - 2)
-    freq = synthetic.rope_freqs(synthetic.mesh_grid_ids(*grid)).to(dev) if grid else None
+    if grid == "per-sample":
+        # sample 0: raster ids of a (1, 2, M/4) grid; sample 1: the same grid
+        # shifted by 7 frames, so every row of the two samples differs
+        ids = synthetic.mesh_grid_ids(1, 2, M // 4)
+        shifted = ids.clone()
+        shifted[0] += 7
+        freq = torch.cat([synthetic.rope_freqs(ids), synthetic.rope_freqs(shifted)]).to(dev)
+        assert freq.shape == (2, M // 2, 1, 64) and not torch.equal(freq[0], freq[1])
+    else:
+        freq = synthetic.rope_freqs(synthetic.mesh_grid_ids(*grid)).to(dev) if grid else None
     plain = ops.linear(x, ws, bs)
     outs, ssqs = ops.linear(x, ws, bs, norm_gamma=gs, norm_freq=freq)
     for i in range(nseg):

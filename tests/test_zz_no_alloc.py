@@ -133,3 +133,42 @@ def test_noalloc_refuses_on_host(dev):
     a.workspace, a.workspace_bytes = ws.data_ptr(), 1024
     assert lib.wam_attention_noalloc(ctypes.byref(a), s) == _lib.WAM_ERR_ARG
     assert "no workspace" in _err()
+
+
+def test_noalloc_under_graph_capture(dev):
+    """What the entry point is for: after one warm-up call (which looks the
+    scratch address up), a call captured into a HIP graph allocates nothing,
+    and every replay equals the eager output bit for bit, with the program's
+    own eager work and synchronisations between the replays."""
+    from wam_ops import _lib
+    from wam_ops.ops import stream_handle
+    lib = _lib.lib()
+    x = _inputs(dev, 4, 1560, 6240, 7)  # a split plan (160 units in 3 key ranges)
+    o_eager = torch.empty_like(x[0])
+    a = _args(*x, o_eager)
+    assert lib.wam_attention_workspace_bytes(a.B, a.Mq, a.H, a.max_keys) > 0
+    assert lib.wam_attention_noalloc(ctypes.byref(a), stream_handle(dev)) == _lib.WAM_OK, _err()
+    torch.cuda.synchronize()
+    o_graph = torch.full_like(x[0], float("nan"))
+    b = _args(*x, o_graph)
+    # torch's own one-time capture state (its generator bookkeeping) comes
+    # with the first capture of the process: capture a torch op once first
+    warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(warm):
+        o_graph.mul_(1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    before = torch.cuda.memory_allocated(dev)
+    with torch.cuda.graph(graph):
+        rc = lib.wam_attention_noalloc(ctypes.byref(b), stream_handle(dev))
+    assert rc == _lib.WAM_OK, _err()
+    grown = torch.cuda.memory_allocated(dev) - before
+    assert grown == 0, f"the captured call allocated {grown} bytes of device memory"
+    for i in range(3):
+        print(f"noalloc graph replay {i}", flush=True)
+        o_graph.fill_(float("nan"))
+        x[0].add_(0)  # eager work on the inputs between replays (values unchanged)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_graph, o_eager), f"replay {i} differs from the eager call"

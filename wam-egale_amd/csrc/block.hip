@@ -199,6 +199,8 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   const int R = B * M;
   WAM_REQUIRE(B >= 1 && M >= 1, "block: empty input B=%d M=%d", B, M);
   WAM_REQUIRE(a->x && a->out, "block: null x/out");
+  WAM_REQUIRE(a->out_dtype == WAM_BF16 || a->out_dtype == WAM_F32, "block: out_dtype %d", a->out_dtype);
+  WAM_REQUIRE(a->out_dtype == WAM_BF16 || !a->debug, "block: debug outputs need the bf16 output");
   WAM_TRY(check_modulation(a->mod, R, "block"));
   WAM_REQUIRE(a->mod.tokens == M && a->mod.temb_mods != 1, "block: temb must be [B, L, 6, D] over M tokens");
   const bool precomputed = a->cross_k && a->cross_v;
@@ -239,12 +241,12 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   // Cross-attention query norm: the projection's epilogue writes y g and the
   // row's sums of squares, attention applies 1/rms (no row pass), when the
   // projection runs as one four-wave launch; other tilings would run the
-  // norm as a pass anyway, and the row pass is as fast.  With debug outputs
-  // requested the queries are normalised by the row pass, so that the debug
-  // copy holds the normalised tensor.  (For the self-attention queries the
-  // same fusion measured even: the QKV epilogue's cost matched the half of
-  // the q/k row pass it removes.)
-  const bool qnorm_fused = a->debug == nullptr && linear_norm_in_epilogue(R, D, 1, D, split_bytes);
+  // norm as a pass anyway, and the row pass is as fast.  A debug call runs
+  // the same kernels; its copies of the projection (before the norm) and of
+  // the normalised queries come from extra debug-only launches.  (For the
+  // self-attention queries the same fusion measured even: the QKV
+  // epilogue's cost matched the half of the q/k row pass it removes.)
+  const bool qnorm_fused = linear_norm_in_epilogue(R, D, 1, D, split_bytes);
   const int qparts = (D + 255) / 256;
 
   wam_modulation mod = a->mod;
@@ -408,15 +410,29 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     if (qnorm_fused) { g.norm_ssq[0] = qssq; g.norm_gamma[0] = W->w[21]; }
     WAM_TRY(linear(&g, s));
-    WAM_TRY(copy_debug(a->debug, 20, cq, rowb, s));
     if (!qnorm_fused) {
+      WAM_TRY(copy_debug(a->debug, 20, cq, rowb, s));
       wam_rms_rope_args r{};
       r.x[0] = cq; r.y[0] = cq; r.gamma[0] = W->w[21]; r.eps[0] = W->eps[5];
       r.ldx = D; r.ldy = D; r.n_tensors = 1; r.rows = R; r.D = D; r.head_dim = W->head_dim;
       WAM_TRY(rms_rope(&r, s));
     }
   }
-  WAM_TRY(copy_debug(a->debug, 7, cq, rowb, s));
+  if (qnorm_fused) {
+    // debug only: the projection before its norm, and the normalised queries
+    // as the reference forms them (the projection, then the RMS row pass:
+    // bf16(y rsqrt(mean y^2 + eps) g), one rounding)
+    if (dbg(20)) WAM_TRY(plain_linear(n2, D, D, 13, -1, dbg(20)));
+    if (dbg(7)) {
+      WAM_TRY(plain_linear(n2, D, D, 13, -1, dbg(7)));
+      wam_rms_rope_args r{};
+      r.x[0] = dbg(7); r.y[0] = dbg(7); r.gamma[0] = W->w[21]; r.eps[0] = W->eps[5];
+      r.ldx = D; r.ldy = D; r.n_tensors = 1; r.rows = R; r.D = D; r.head_dim = W->head_dim;
+      WAM_TRY(rms_rope(&r, s));
+    }
+  } else {
+    WAM_TRY(copy_debug(a->debug, 7, cq, rowb, s));
+  }
   // 10. Cross K/V: precomputed or from the context.
   const void* ck = a->cross_k;
   const void* cv = a->cross_v;
@@ -493,6 +509,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
       g.w[0] = W->ffn_fp8[1]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[1];
     }
     g.gate = mod; g.gate_index = 5;
+    g.out_dtype = a->out_dtype;
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }

@@ -735,7 +735,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   constexpr bool PART = EPI == kEpiPartial;
   constexpr int RB = RF32 ? 4 : 2;                 // residual bytes per element
   constexpr int OB = (OF32 || PART) ? 4 : 2;       // output bytes per element
-  const uint32_t rows_left = (uint32_t)(p.M - m0);
+  // Rows of this tile that exist (the resources start at row m0, so their
+  // bounds cover at most TM rows and stay far below 2^32 bytes).
+  const uint32_t rows_left = (uint32_t)min(p.M - m0, TM);
   // (without a residual the resource is a zero-length one over the output; never read)
   const __amdgpu_buffer_rsrc_t rres =
       RES ? make_rsrc(static_cast<const char*>(p.res) + ((int64_t)m0 * p.ldr + n0) * RB,
@@ -1289,6 +1291,9 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a->a != nullptr, "wam_linear: null activation");
   WAM_REQUIRE((int64_t)a->M * a->lda * 2 < (int64_t)1 << 31 && (int64_t)a->seg_n * a->ldw * wb < (int64_t)1 << 31,
               "wam_linear: operands above 2 GiB are not supported");
+  // Epilogue addresses within one tile (up to 256 rows of fp32) are 32-bit.
+  WAM_REQUIRE(a->ldo < ((int64_t)1 << 21) && a->ldr < ((int64_t)1 << 21),
+              "wam_linear: output/residual row strides must be below 2^21 elements");
   for (int i = 0; i < a->n_seg; ++i) {
     WAM_REQUIRE(a->w[i] != nullptr && a->out[i] != nullptr, "wam_linear: null weight/out %d", i);
     WAM_REQUIRE(!f8 || a->w_scale[i] != nullptr, "wam_linear: fp8 weights need w_scale %d", i);

@@ -5,7 +5,6 @@ compares every ``sizeof`` with the library's own (``wam_abi_struct_size``).
 There is no fallback: if the library is missing, every entry point raises.
 """
 import ctypes
-import os
 from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64,
                     c_size_t, c_uint32, c_void_p)
 from functools import lru_cache
@@ -104,7 +103,8 @@ class BlockArgs(Structure):
                 ("cache_is_pred", c_void_p), ("cache_batch", c_int), ("pool", c_int),
                 ("candidate_rows", c_void_p), ("update", c_int), ("cross_k", c_void_p),
                 ("cross_v", c_void_p), ("out", c_void_p), ("workspace", c_void_p),
-                ("workspace_bytes", c_size_t), ("debug", c_void_p), ("timer", c_void_p)]
+                ("workspace_bytes", c_size_t), ("debug", c_void_p), ("timer", c_void_p),
+                ("out_dtype", c_int)]
 
 
 class PatchifyArgs(Structure):
@@ -179,7 +179,7 @@ class NativeLibraryMissing(RuntimeError):
 @lru_cache(None)
 def lib():
     """Load the in-tree HIP library; raise if it has not been built."""
-    path = Path(os.environ.get("WAM_BLOCK_LIB", LIB_PATH))
+    path = LIB_PATH
     if not path.exists():
         raise NativeLibraryMissing(
             f"{path} is missing: build the HIP library first (python -c "

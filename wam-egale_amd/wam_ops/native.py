@@ -118,7 +118,9 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     ``rows_checked``: the caller has already validated the candidate rows'
     values against this cache's batch (no host read-back here).
     ``workspace``: a uint8 device tensor to use if it is large enough.
-    ``out``: a preallocated [B, M, D] bf16 output (must not alias the input)."""
+    ``out``: a preallocated [B, M, D] output (must not alias the input):
+    bf16, or fp32 for the block's result before its final bf16 rounding (a
+    parity diagnostic; not with ``debug``)."""
     x = hidden_states
     dev = bound.device
     _check(x.is_cuda and x.device == dev and x.dtype == torch.bfloat16 and x.is_contiguous()
@@ -184,10 +186,12 @@ def run_block(bound, hidden_states, encoder_hidden_states, temb, rotary_emb, cac
     if out is None:
         out = torch.empty_like(x)
     else:
-        _check(out.shape == x.shape and out.dtype == x.dtype and out.device == dev
+        _check(out.shape == x.shape and out.dtype in (torch.bfloat16, torch.float32) and out.device == dev
                and out.is_contiguous() and out.data_ptr() != x.data_ptr(),
-               "out must be a separate [B, M, D] bf16 tensor")
+               "out must be a separate [B, M, D] bf16 or fp32 tensor")
+        _check(out.dtype == torch.bfloat16 or not debug, "debug outputs need a bf16 out")
     args.out = out.data_ptr()
+    args.out_dtype = dtype_code(out)
     nbytes = _lib.lib().wam_block_workspace_bytes(B, M, D, bound.ffn_dim, ctx.shape[0],
                                                    ctx.shape[1], pool)
     if workspace is not None and workspace.numel() >= nbytes and workspace.device == dev:
