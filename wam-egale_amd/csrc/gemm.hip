@@ -528,6 +528,16 @@ struct CfgW4t224 {
   static constexpr int BM = 224, BN = 256, BK = 64, WB = 2, kThreads = 256;
   static constexpr bool kW4 = true;
 };
+// The same two tilings with fp8 e4m3 weights (widened to bf16 on the way
+// into LDS; per-column scales in the epilogue).
+struct CfgW4f8 {
+  static constexpr int BM = 256, BN = 256, BK = 64, WB = 1, kThreads = 256;
+  static constexpr bool kW4 = true;
+};
+struct CfgW4t224f8 {
+  static constexpr int BM = 224, BN = 256, BK = 64, WB = 1, kThreads = 256;
+  static constexpr bool kW4 = true;
+};
 
 // The NM MFMAs of one 16-deep sub-step with the NR fragment reads of the
 // next sub-step, W LDS writes and V global loads spread evenly between them
@@ -546,14 +556,22 @@ __device__ __forceinline__ void w4_sched() {
 // RF32 / OF32: the residual / output is fp32 (else bf16); compile-time so
 // that the epilogue's loads and stores are branch-free.  TM: tile rows, 256
 // (waves 2 x 2, 128 x 128 each) or 224 (waves 1 x 4, 224 x 64 each).
-template <int EPI, int RF32, int OF32, int TM>
+// WB: bytes per weight element, 2 (bf16) or 1 (fp8 e4m3 with per-column
+// fp32 scales).  fp8 weight rows are 64 bytes per k-step: a thread loads 16
+// of them (a quarter row) and widens them exactly to bf16 in registers as it
+// writes the stage, so the LDS layout and the MFMA loop are those of bf16;
+// the scale multiplies the fp32 sums in the epilogue.
+template <int EPI, int RF32, int OF32, int TM, int WB = 2>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   static_assert(TM == 256 || TM == 224, "tile rows");
+  static_assert(WB == 2 || WB == 1, "weight bytes");
   constexpr int MB = TM == 256 ? 4 : 7;   // 32-row m-blocks per wave
   constexpr int NB = TM == 256 ? 4 : 2;   // 32-column n-blocks per wave
   constexpr int WGN = TM == 256 ? 2 : 4;  // waves along n
   constexpr int LA = TM / 32;             // A staging loads per thread and k-step
-  constexpr int NL = LA + 8;              // and the 8 of W
+  constexpr int LW = WB == 2 ? 8 : 4;     // W staging loads per thread and k-step
+  constexpr int NL = LA + LW;
+  constexpr int WKB = 64 * WB;            // bytes of a weight row per k-step
   constexpr int NM = MB * NB, NR = MB + NB;  // MFMAs and fragment reads per sub-step
   __shared__ __attribute__((aligned(1024))) char L0[65536];
   __shared__ __attribute__((aligned(1024))) char L1[65536];
@@ -590,19 +608,24 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   // segment's N (W) load as zeros through the bound.
   const char* wseg = static_cast<const char*>(seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]));
   const char* abase = reinterpret_cast<const char*>(p.a + (int64_t)m0 * p.lda) + kb * 128;
-  const char* bbase = wseg + (int64_t)n0 * p.ldw * 2 + kb * 128;
+  const char* bbase = wseg + (int64_t)n0 * p.ldw * WB + kb * WKB;
   const uint32_t abytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u - (uint32_t)kb * 128u;
-  const uint32_t bbytes = (uint32_t)min(256, p.seg_n - n0) * (uint32_t)p.ldw * 2u - (uint32_t)kb * 128u;
+  const uint32_t bbytes =
+      (uint32_t)min(256, p.seg_n - n0) * (uint32_t)p.ldw * (uint32_t)WB - (uint32_t)kb * (uint32_t)WKB;
   auto res_a = [&](int kt) { return make_rsrc(abase + kt * 128, abytes - (uint32_t)kt * 128u); };
-  auto res_b = [&](int kt) { return make_rsrc(bbase + kt * 128, bbytes - (uint32_t)kt * 128u); };
+  auto res_b = [&](int kt) { return make_rsrc(bbase + kt * WKB, bbytes - (uint32_t)kt * (uint32_t)WKB); };
 
   // Staging: load i (0..NL-1) of a thread is row 32 i + tid / 8 of A (i < LA)
   // or row 32 (i - LA) + tid / 8 of W, 16-byte chunk tid % 8.  Its LDS slot
   // is that row's chunk under the swizzle; (row >> 1) & 7 does not depend on i.
+  // fp8 weights: W load j is row 64 j + tid / 4, bytes 16 (tid % 4) .. +16,
+  // i.e. the bf16 chunks 2 (tid % 4) and 2 (tid % 4) + 1 of that row.
   const int lr = tid >> 3, lc = tid & 7;
-  const int va = lr * (int)p.lda * 2 + lc * 16, vb = lr * (int)p.ldw * 2 + lc * 16;
-  const int ra32 = 32 * (int)p.lda * 2, rb32 = 32 * (int)p.ldw * 2;
+  const int va = lr * (int)p.lda * 2 + lc * 16;
+  const int vb = WB == 2 ? lr * (int)p.ldw * 2 + lc * 16 : (tid >> 2) * (int)p.ldw + (tid & 3) * 16;
+  const int ra32 = 32 * (int)p.lda * 2, rb32 = (WB == 2 ? 32 : 64) * (int)p.ldw * WB;
   const int wofs = lds_off<8>(lr, lc);
+  const int wofs8_0 = lds_off<8>(tid >> 2, 2 * (tid & 3)), wofs8_1 = lds_off<8>(tid >> 2, 2 * (tid & 3) + 1);
   typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
   u32x4s S0[NL], S1[NL];
   auto gload = [&](u32x4s* S, int kt, auto lo_c, auto hi_c) {
@@ -617,11 +640,24 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   auto swrite = [&](u32x4s* S, char* buf, auto lo_c, auto hi_c) {
     constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
 #pragma unroll
-    for (int i = LO; i < HI; ++i)
-      *reinterpret_cast<u32x4s*>(buf + (i >= LA ? 32768 + (i - LA) * 4096 : i * 4096) + wofs) = S[i];
+    for (int i = LO; i < HI; ++i) {
+      if (WB == 2 || i < LA) {
+        *reinterpret_cast<u32x4s*>(buf + (i >= LA ? 32768 + (i - LA) * 4096 : i * 4096) + wofs) = S[i];
+      } else {
+        char* w = buf + 32768 + (i - LA) * 8192;
+        *reinterpret_cast<bf16x8*>(w + wofs8_0) = fp8x8_to_bf16x8(u32x2{S[i][0], S[i][1]});
+        *reinterpret_cast<bf16x8*>(w + wofs8_1) = fp8x8_to_bf16x8(u32x2{S[i][2], S[i][3]});
+      }
+    }
+  };
+  // LDS writes of staging slots [lo, hi): one per slot, two per fp8 W slot.
+  constexpr auto dsw = [](int lo, int hi) {
+    int n = 0;
+    for (int i = lo; i < hi; ++i) n += (WB == 1 && i >= LA) ? 2 : 1;
+    return n;
   };
   // The staging sets go to LDS and are reloaded in three parts over a k-step.
-  constexpr int P1 = NL == 16 ? 6 : 5, P2 = NL == 16 ? 11 : 10;
+  constexpr int P1 = WB == 1 ? 5 : (NL == 16 ? 6 : 5), P2 = WB == 1 ? 9 : (NL == 16 ? 11 : 10);
   using I0 = std::integral_constant<int, 0>;
   using IP1 = std::integral_constant<int, P1>;
   using IP2 = std::integral_constant<int, P2>;
@@ -671,19 +707,19 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     rd(cur, 1, 1);
     swrite(Snext, nxt, I0{}, IP1{});
     mm(0);
-    w4_sched<P1, 0, NM, NR>();
+    w4_sched<dsw(0, P1), 0, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     rd(cur, 2, 0);
     swrite(Snext, nxt, IP1{}, IP2{});
     gload(Snext, kt3, I0{}, IP1{});
     mm(1);
-    w4_sched<P2 - P1, P1, NM, NR>();
+    w4_sched<dsw(P1, P2), P1, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     rd(cur, 3, 1);
     swrite(Snext, nxt, IP2{}, INL{});
     gload(Snext, kt3, IP1{}, IP2{});
     mm(0);
-    w4_sched<NL - P2, P2 - P1, NM, NR>();
+    w4_sched<dsw(P2, NL), P2 - P1, NM, NR>();
     __builtin_amdgcn_sched_barrier(0);
     // Every wave has written its part of the next stage and read its last
     // fragments of this one.
@@ -724,6 +760,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(tb[e]);
     }
+  }
+  float wsc[4] = {1.f, 1.f, 1.f, 1.f};  // fp8 weight scales of the lane's columns
+  if constexpr (WB == 1 && EPI != kEpiPartial) {
+    const float4 t = *reinterpret_cast<const float4*>((seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2])) + n);
+    wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
   float gate[4] = {0.f, 0.f, 0.f, 0.f};
   bool gate_once = false;
@@ -889,7 +930,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
         }
         float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = vv[k8][e] + bv[e];
+        for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? vv[k8][e] * wsc[e] + bv[e] : vv[k8][e] + bv[e];
         if constexpr (EPI == WAM_EPI_BIAS_GELU) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
@@ -994,9 +1035,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
 using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
 using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
 using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
-// fp8 e4m3 weights (64-byte LDS weight rows, two stages, loads issued in
-// two parts)
-using Cfg256x256f8s = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 1, 2>;
+// fp8 e4m3 weights on the small tiles (64-byte LDS weight rows widened at
+// the fragment read); the big tiles run the four-wave kernel.
 using Cfg128x128f8 = GemmCfg<128, 128, 64, 2, 2, 3, 1, 0, 1>;
 
 // Sum of the k_split fp32 partial ranges of a split-K launch (in range
@@ -1089,15 +1129,15 @@ static void launch_tiles(dim3 grid, const LinearParams& p, hipStream_t s) {
     constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
     if constexpr (RES) {
       if (p.res_f32 && p.out_f32)
-        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 1, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 1, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
       else if (p.res_f32)
-        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 1, 0, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
       else if (p.out_f32)
-        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 1, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 1, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
       else
-        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
     } else {
-      hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM>), grid, dim3(C::kThreads), 0, s, p);
+      hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
     }
   } else {
     hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI>), grid, dim3(C::kThreads), 0, s, p);
@@ -1357,7 +1397,14 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   }
   const bool big = uses_big_tiles(a->M, a->seg_n, a->n_seg);
   if (f8) {
-    if (big) return launch_big<Cfg256x256f8s, Cfg128x128f8>(p, ws_bytes, s);
+    // fp8 weights: the four-wave kernel widens them to bf16 as it stages
+    // them (FFN unit at 4680 rows, alternating runs on one box: 713-714 us
+    // with the eight-wave kernel, 678 us with this one; bf16 679-680 us)
+    if (big) {
+      if (w4_t224_wins(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes))
+        return launch_gemm<CfgW4t224f8>(p, s);
+      return launch_big<CfgW4f8, Cfg128x128f8>(p, ws_bytes, s);
+    }
     return launch_gemm<Cfg128x128f8>(p, s);
   }
   // Big tiles when the grid still covers the chip; otherwise smaller tiles.
