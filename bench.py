@@ -268,7 +268,9 @@ def _unit(ms, flop):
 
 def c4a_attention(shape, dev, steps, warmup, q_tokens=1560, prefix=6240):
     """Self attention of 1560 new tokens over a 6240-token cached prefix (pool
-    row 0 through the slot list) plus themselves, 24 x 128 heads; N(0, 1) Q/K/V."""
+    row 0, slots 0..6239) plus themselves, 24 x 128 heads; N(0, 1) Q/K/V.  The
+    history base is passed as the block passes kv_layout's info[2] (the
+    prefix is one run of consecutive slots)."""
     import torch
     from wam_ops import ops
     H = shape.heads
@@ -280,7 +282,9 @@ def c4a_attention(shape, dev, steps, warmup, q_tokens=1560, prefix=6240):
     pv = torch.randn(1, prefix, H, 128, generator=g, device=dev).to(torch.bfloat16)
     slots = torch.arange(prefix, dtype=torch.int32, device=dev)
     n_hist = torch.tensor([prefix], dtype=torch.int32, device=dev)
-    ms = timed_steps(lambda: ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n_hist),
+    base = torch.zeros(1, dtype=torch.int32, device=dev)
+    ms = timed_steps(lambda: ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n_hist,
+                                           hist_base=base),
                      steps, warmup, gate="C4a self attention")
     return _unit(ms, 4 * q_tokens * (prefix + q_tokens) * shape.dim)
 

@@ -203,6 +203,8 @@ int wam_rms_rope(const wam_rms_rope_args* args, void* stream);
 /* O[b, i, h, :] = softmax_j(Q[b,i,h,:] . K_j / sqrt(hd)) V_j over the key list
  *   j <  n_hist : pool row pool_rows[b] (or b), slot slots[j]
  *   j >= n_hist : own key (j - n_hist) of own batch row kv_rows[b] (or b)
+ * Slots address rows within one pool row block: slots[j] * pool_rstride <
+ * pool_bstride (a [Bp, P, H, 128] pool has pool_bstride = P * pool_rstride).
  * n_hist is read from device memory (n_hist_dev) so the host never waits for
  * the slot compaction.  Non-causal, like model.py:37-40. */
 typedef struct {
@@ -229,6 +231,12 @@ typedef struct {
    * + q_eps), applied to its scores (which are linear in Q).  q_ssq_n <= 16.
    * The reference normalises Q in a separate pass (model.py:609-612). */
   const float* q_ssq; int q_ssq_n; int q_norm_dim; float q_eps;
+  /* Optional device int (kv_layout's info[2]): when it holds s >= 0, the
+   * history is slots s, s + 1, ..., s + n_hist - 1 in that order, i.e.
+   * slots[j] == s + j, and the kernel reads the pool rows at that base
+   * without the slot list; -1 (or a NULL pointer) reads them through slots.
+   * No counterpart in the reference, which gathers the valid rows. */
+  const int32_t* hist_base_dev;
 } wam_attention_args;
 
 int wam_attention(const wam_attention_args* args, void* stream);
@@ -256,7 +264,9 @@ int wam_attention_noalloc(const wam_attention_args* args, void* stream);
  *  candidate == 1: read only.
  * Always: hist_slots = the valid slots before the new ones, in ascending
  * order, and n_hist their count.  info[0] = n_hist, info[1] = error code
- * (0 ok, 2 invalid candidate row).  Runs as one workgroup; no host sync. */
+ * (0 ok, 2 invalid candidate row), info[2] = hist_slots[0] when the history
+ * is one run of consecutive slots (hist_slots[j] == hist_slots[0] + j), else
+ * -1 (attention's hist_base_dev).  Runs as one workgroup; no host sync. */
 typedef struct {
   uint8_t* mask; int64_t* ids; uint8_t* is_pred; int pool;
   int tokens; int update; int candidate;

@@ -331,6 +331,57 @@ def test_attention_history(dev, B, Mq, P, nvalid, Bp, candidate):
     assert_close(o, ref, 2e-2, 0.9999, "history attention")
 
 
+# History in consecutive slots (kv_layout's info[2] >= 0): the pipelined
+# kernel reads the pool rows at that base, without the slot list.  Same keys
+# in the same order as through the slot list, so the outputs are bitwise
+# equal; n_hist % 4 != 0 puts the last pool keys in a block that straddles
+# the own keys; a base of 0 and a base inside the pool; the C4a shape.
+@pytest.mark.parametrize("B,Mq,P,base,nvalid,Bp", [(4, 1560, 7800, 0, 6240, 1), (2, 1000, 3000, 700, 1237, 2),
+                                                   (1, 1560, 7800, 0, 6240, 1), (2, 1300, 2000, 3, 1, 2)])
+def test_attention_consecutive_history(dev, B, Mq, P, base, nvalid, Bp):
+    from wam_ops import ops
+    H = 24
+    q = _randn((B, Mq, H, 128), dev, 11)
+    k = _randn((B, Mq, H, 128), dev, 12)
+    v = _randn((B, Mq, H, 128), dev, 13)
+    pk = _randn((Bp, P, H, 128), dev, 14)
+    pv = _randn((Bp, P, H, 128), dev, 15)
+    slots = torch.arange(base, base + nvalid, dtype=torch.int32, device=dev)
+    n = torch.tensor([nvalid], dtype=torch.int32, device=dev)
+    rows = torch.tensor([(i + 1) % Bp for i in range(B)], dtype=torch.int64, device=dev)
+    via_slots = ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n, pool_rows=rows)
+    hb = torch.tensor([base], dtype=torch.int32, device=dev)
+    at_base = ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n, pool_rows=rows, hist_base=hb)
+    assert torch.equal(at_base, via_slots), "consecutive-history path differs from the slot-list path"
+    none = torch.tensor([-1], dtype=torch.int32, device=dev)
+    assert torch.equal(ops.attention(q, k, v, pool_k=pk, pool_v=pv, slots=slots, n_hist=n, pool_rows=rows,
+                                     hist_base=none), via_slots)
+    hk = pk[:, base:base + nvalid].index_select(0, rows)
+    hv = pv[:, base:base + nvalid].index_select(0, rows)
+    ref = _ref_attn(q, torch.cat([hk, k], 1), torch.cat([hv, v], 1))
+    assert_close(at_base, ref, 2e-2, 0.9999, "consecutive history attention")
+
+
+def test_kv_layout_reports_consecutive_history(dev):
+    """info[2]: the first history slot when the valid slots form one run,
+    else -1."""
+    from wam_ops import ops
+    P, H = 64, 1
+    for valid, expect in (((3, 4, 5, 6), 3), ((0, 1, 2), 0), ((2, 3, 5), -1), ((), -1)):
+        cache = {"k": torch.zeros(1, P, H, 128, dtype=torch.bfloat16, device=dev),
+                 "v": torch.zeros(1, P, H, 128, dtype=torch.bfloat16, device=dev),
+                 "id": torch.full((P,), -1, dtype=torch.int64, device=dev),
+                 "mask": torch.zeros(P, dtype=torch.bool, device=dev),
+                 "is_pred": torch.zeros(P, dtype=torch.bool, device=dev)}
+        for i in valid:
+            cache["mask"][i] = True
+            cache["id"][i] = 0
+        rows = torch.zeros(1, dtype=torch.int64, device=dev)
+        res = ops.kv_layout(cache, 4, 0, candidate_rows=rows)
+        info = res[-1].cpu()
+        assert info[0].item() == len(valid) and info[2].item() == expect, (valid, info.tolist())
+
+
 def _cache_pair(P, H, seed, dev, prefix_chunks):
     """Identical CPU (oracle) and GPU pools after committing some chunks."""
     c = okv.new_cache(P, H, 128, 1, torch.bfloat16)

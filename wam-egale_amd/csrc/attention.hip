@@ -440,6 +440,9 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   // bytes per pool row (the host only picks this kernel when it fits 32 bits)
   const uint32_t pool_row_bytes = (uint32_t)a.pool_rstride * 2u;
   const i32x4 rk = make_rsrc4(kbase, kv_bytes), rv = make_rsrc4(vbase, kv_bytes);
+  // History in consecutive slots (kv_layout's info[2] = its first slot):
+  // slot = base + key index, so no slot list is copied or read.
+  const int hbase = HIST && a.hist_base_dev ? __builtin_amdgcn_readfirstlane(*a.hist_base_dev) : -1;
   const bf16* qbase = static_cast<const bf16*>(a.q) + (int64_t)b * a.q_bstride + h * kAttnHD;
   const __amdgpu_buffer_rsrc_t rq =
       make_rsrc(qbase, (uint32_t)(((int64_t)(a.Mq - 1) * a.q_rstride + kAttnHD) * 2));
@@ -460,9 +463,12 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   // 4 (blk & 3) + L/16 for K, (row & 3) = L/16 for V.  Keys past the end read
   // own key Mk - 1 (finite values; their probabilities are zero).  Own keys go
   // through buffer loads with 32-bit byte offsets (the host only picks this
-  // kernel when they fit); a block that holds pool keys uses 64-bit per-lane
-  // addresses, with the slots of its rows read from the stage's slot list in
-  // LDS (load_slots, one step ahead).
+  // kernel when they fit); a block of pool keys loads from the pool row base
+  // in SGPRs plus slot * row bytes in 32 bits, with the slots of its rows
+  // read from the stage's slot list in LDS (load_slots, one step ahead), or
+  // formed as base + key index when the history is consecutive slots.  Per
+  // tile and wave, against 64-bit per-lane addresses: 22 -> 14 spilled SGPRs
+  // (to VGPR lanes); C4a 234.6 -> 232.9 us, verify layer 2647 -> 2641 us.
   constexpr int kSub = (32 + NW - 1) / NW;  // sub-block slots per wave
   const int nsub = (32 - wave + NW - 1) / NW;
   const int lr = lane >> 4, pch = lane & 15;
@@ -472,7 +478,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   // The last wave (one of those with the fewest sub-blocks) copies the 64
   // slots of tile T into the list of its stage: lane L slot T*64 + L.
   auto load_slots = [&](int T, int st_bytes) {
-    if (HIST && wave == NW - 1 && T * kAttnKT < n_hist) {
+    if (HIST && hbase < 0 && wave == NW - 1 && T * kAttnKT < n_hist) {
       const int* src = slots + min(T * kAttnKT + lane, n_hist - 1);
       asm_g_ld4_lds((uint64_t)(uintptr_t)src, slot_list(st_bytes));
     }
@@ -491,16 +497,25 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
       if (!HIST || j0 >= n_hist) {
         const int row = min(j0 + lr - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2;
         asm_ld16_lds(isk ? rk : rv, dst, row + lc);
-      } else {
+      } else if (j0 + 4 <= n_hist) {
+        // four pool keys: pool row base (SGPRs) + slot * row bytes (32-bit;
+        // the host only picks this kernel when a pool row block fits)
         const int j = j0 + lr;
-        const int slot = *reinterpret_cast<const int*>(slot_list(st_bytes) + (4 * blk + lr) * 4);
-        // pool row: base + slot * row bytes (one 32 x 32 -> 64-bit
-        // multiply-add); own row: base + a 32-bit offset
-        const uint64_t pb0 = (uint64_t)(uintptr_t)(isk ? pkbase : pvbase) + (uint32_t)lc;
-        const uint64_t ob0 = (uint64_t)(uintptr_t)(isk ? kbase : vbase) + (uint32_t)lc;
-        const uint64_t src = j < n_hist ? pb0 + (uint64_t)(uint32_t)slot * pool_row_bytes
-                                        : ob0 + (uint32_t)(min(j - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2);
-        asm_g_ld16_lds(src, dst);
+        const int slot = hbase >= 0 ? hbase + j
+                                    : *reinterpret_cast<const int*>(slot_list(st_bytes) + (4 * blk + lr) * 4);
+        asm_gs_ld16_lds(isk ? pkbase : pvbase, (uint32_t)slot * pool_row_bytes + (uint32_t)lc, dst);
+      } else {
+        // the block that holds the last pool keys and the first own keys:
+        // two loads under complementary lane masks (one more load in this
+        // tile; the per-tile waits then wait for it too, never too little)
+        const int j = j0 + lr;
+        if (j < n_hist) {
+          const int slot = hbase >= 0 ? hbase + j
+                                      : *reinterpret_cast<const int*>(slot_list(st_bytes) + (4 * blk + lr) * 4);
+          asm_gs_ld16_lds(isk ? pkbase : pvbase, (uint32_t)slot * pool_row_bytes + (uint32_t)lc, dst);
+        } else {
+          asm_ld16_lds(isk ? rk : rv, dst, min(j - n_hist, a.Mk - 1) * (int)a.kv_rstride * 2 + lc);
+        }
       }
     }
   };
@@ -942,14 +957,14 @@ static AttnPlan attention_plan(int B, int Mq, int H, int64_t keys, int64_t max_b
 static bool g_attn_w4 = true;
 
 // The pipelined kernel runs when every Q and own K/V row's byte offset fits in
-// 31 bits (pool rows use 64-bit addresses, with a pool row's bytes in 32 bits)
-// and the query grid is at least 128
-// units of 256 rows; smaller grids use attention_kernel<4>.
+// 31 bits, the pool rows of one batch row (slots < pool_bstride /
+// pool_rstride) in 32 bits, and the query grid is at least 128 units of 256
+// rows; smaller grids use attention_kernel<4>.
 static bool sp_eligible(const wam_attention_args* a) {
   const int64_t grid8 = (int64_t)((a->Mq + 255) / 256) * a->H * a->B;
   return g_attn_w4 && grid8 >= 128 && ((int64_t)a->Mq + 256) * a->q_rstride * 2 < (int64_t)INT32_MAX &&
          ((int64_t)a->Mk + kAttnKT) * a->kv_rstride * 2 < (int64_t)INT32_MAX &&
-         a->pool_rstride * 2 <= (int64_t)UINT32_MAX;
+         (!a->n_hist_dev || (a->pool_bstride >= a->pool_rstride && a->pool_bstride * 2 < (int64_t)UINT32_MAX));
 }
 
 // Query rows per unit of the pipelined kernel: 224 (7 waves) when its plan
@@ -965,10 +980,10 @@ static int sp_query_tile(int B, int Mq, int H, int64_t keys) {
   return p224.cost <= p256.cost + 1e-9 ? 224 : 256;
 }
 
-// Calls with pool keys keep 256-query units: the pool path's per-lane 64-bit
-// addresses leave the 7-wave kernel short of registers (it spilled to scratch
-// inside the key loop), and a 224-query unit takes as long as a 256-query one
-// on the SIMDs that hold two of its waves.
+// Calls with pool keys keep 256-query units: the pool path leaves the 7-wave
+// kernel short of registers (with 32-bit pool offsets it still spills 14
+// VGPRs to scratch), and a 224-query unit takes as long as a 256-query one on
+// the SIMDs that hold two of its waves.
 static int query_tile(const wam_attention_args* a, int64_t keys) {
   return sp_eligible(a) && a->n_hist_dev == nullptr ? sp_query_tile(a->B, a->Mq, a->H, keys) : 256;
 }

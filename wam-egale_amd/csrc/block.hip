@@ -355,6 +355,7 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
       t.pool_k = a->cache_k; t.pool_v = a->cache_v;
       t.pool_rstride = D; t.pool_bstride = (int64_t)a->pool * D; t.pool_batch = a->cache_batch;
       t.slots = slots; t.n_hist_dev = info; t.pool_rows = a->candidate_rows;
+      t.hist_base_dev = info + 2;
     }
     t.k = qkv + D; t.v = qkv + 2 * D; t.kv_bstride = (int64_t)M * 3 * D; t.kv_rstride = 3 * D;
     t.Mk = M; t.kv_batch = B;

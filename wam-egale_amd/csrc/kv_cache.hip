@@ -139,6 +139,16 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   int tv, tf;
   int pv = block_excl_scan(nv, sh_i, &tv);
   int pf = block_excl_scan(nf, sh_i, &tf);
+  // Is the history one run of consecutive slots?  (Its first and last valid
+  // slots, before this call's new slots are marked.)
+  long long first = 0x7fffffffffffffffLL, lastv = -1;
+  for (int i = lo; i < hi; ++i)
+    if (a.mask[i]) {
+      first = min(first, (long long)i);
+      lastv = max(lastv, (long long)i);
+    }
+  first = block_reduce_ll(first, false, sh_ll);
+  lastv = block_reduce_ll(lastv, true, sh_ll);
   for (int i = lo; i < hi; ++i) {
     const bool valid = a.mask[i];
     if (valid) a.hist_slots[pv++] = i;
@@ -155,6 +165,7 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   if (tid == 0) {
     a.info[0] = tv;
     a.info[1] = error;
+    a.info[2] = (tv > 0 && lastv - first + 1 == tv) ? (int)first : -1;
   }
 }
 

@@ -165,6 +165,15 @@ __device__ inline void asm_g_ld16_lds(uint64_t gaddr, void* lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gaddr), "{m0}"(m0) : "memory");
 }
 
+// Same from a wave-uniform 64-bit base (in SGPRs) plus a per-lane 32-bit byte
+// offset: one VGPR of address per lane instead of two.  Four wait states
+// cover an SGPR of the base written by a VALU instruction just before.
+__device__ inline void asm_gs_ld16_lds(const void* base, uint32_t voff, void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  const uint64_t b = reinterpret_cast<uint64_t>(uniform_ptr(base));
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" :: "v"(voff), "s"(b), "{m0}"(m0) : "memory");
+}
+
 // 4 bytes per lane from a per-lane 64-bit global address into LDS
 // (global_load_lds_dword): lane L writes bytes [4 L, 4 L + 4) at `lds`.
 __device__ inline void asm_g_ld4_lds(uint64_t gaddr, void* lds) {
@@ -293,10 +302,14 @@ __device__ inline void wave_sum8(const float v[8], float out[2]) {
 }
 
 // GELU, tanh approximation: 0.5 x (1 + tanh(u)) = x * sigmoid(2u),
-// u = sqrt(2/pi) (x + 0.044715 x^3).  sigmoid via v_exp_f32 and v_rcp_f32.
+// u = sqrt(2/pi) (x + 0.044715 x^3).  sigmoid via v_exp_f32 and v_rcp_f32,
+// with the constants folded: -2 log2(e) u = x (A + B x^2), so an output is
+// x^2, one FMA, one multiply, the exponential, an add, the reciprocal and a
+// multiply.
 __device__ inline float gelu_tanh(float x) {
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float e = __builtin_amdgcn_exp2f(-2.0f * kLog2e * u);
+  constexpr float A = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+  constexpr float B = A * 0.044715f;
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(x * x, B, A));
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

@@ -72,7 +72,8 @@ class AttentionArgs(Structure):
                 ("v", c_void_p), ("kv_bstride", c_int64), ("kv_rstride", c_int64),
                 ("Mk", c_int), ("kv_rows", c_void_p), ("kv_batch", c_int), ("scale", c_float),
                 ("workspace", c_void_p), ("workspace_bytes", c_int64), ("max_keys", c_int),
-                ("q_ssq", c_void_p), ("q_ssq_n", c_int), ("q_norm_dim", c_int), ("q_eps", c_float)]
+                ("q_ssq", c_void_p), ("q_ssq_n", c_int), ("q_norm_dim", c_int), ("q_eps", c_float),
+                ("hist_base_dev", c_void_p)]
 
 
 class KvLayoutArgs(Structure):

@@ -275,7 +275,7 @@ def rms_rope(tensors, gammas, eps, freq=None, head_dim=128, out=None):
 
 
 def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, pool_rows=None,
-              kv_rows=None, scale=None, out=None, q_ssq=None, q_eps=1e-6):
+              kv_rows=None, scale=None, out=None, q_ssq=None, q_eps=1e-6, hist_base=None):
     """softmax(q [history || k]^T / sqrt(hd)) [history || v] per head.
 
     q [B, Mq, H, 128]; k, v [Bk, Mk, H, 128] (any row stride, unit last dim);
@@ -283,7 +283,10 @@ def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, poo
     pool row pool_rows[b] (int64) or b; own row kv_rows[b] or b.
     q_ssq: fp32 [B * Mq, n] partial sums of squares of each query row (the
     norm epilogue of linear); query rows are then scaled by
-    rsqrt(sum / (H * 128) + q_eps) (RMSNorm across heads)."""
+    rsqrt(sum / (H * 128) + q_eps) (RMSNorm across heads).
+    hist_base: int32 device scalar (kv_layout's info[2]); when it holds
+    s >= 0 the caller asserts slots[j] == s + j and the kernel reads the pool
+    rows at that base instead of through the slot list."""
     dev = _dev(q, k, v, pool_k, pool_v, slots, n_hist, pool_rows, kv_rows)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _bf16(t, n)
@@ -305,6 +308,9 @@ def attention(q, k, v, *, pool_k=None, pool_v=None, slots=None, n_hist=None, poo
         a.pool_bstride, a.pool_rstride = pool_k.stride(0), pool_k.stride(1)
         a.pool_batch = pool_k.shape[0]
         a.slots, a.n_hist_dev = slots.data_ptr(), n_hist.data_ptr()
+        if hist_base is not None:
+            _req(hist_base.dtype == torch.int32 and hist_base.device == dev, "hist_base is an int32 device scalar")
+            a.hist_base_dev = hist_base.data_ptr()
         if pool_rows is not None:
             _req(pool_rows.dtype == torch.int64 and pool_rows.numel() == B, "pool_rows int64 [B]")
             a.pool_rows = pool_rows.data_ptr()
