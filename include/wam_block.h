@@ -153,6 +153,14 @@ typedef struct {
    * separate row pass. */
   float* norm_ssq[3]; const void* norm_gamma[3];
   const void* norm_freq; int norm_freq_batch, norm_tokens, norm_head_dim;
+  /* Activation storage.  WAM_BF16, or WAM_FP8: a is e4m3 [M, K] (lda in
+   * elements = bytes) with one fp32 scale per row (a_scale[m], e.g. absmax/448
+   * from wam_quantize_fp8_rows), and the product runs on the fp8 MFMA:
+   * y = sum_k fp8(a[m,k]) fp8(w[n,k]) * a_scale[m] * w_scale[n] + b[n].
+   * Needs fp8 weights, WAM_EPI_BIAS or WAM_EPI_BIAS_GELU, one segment of
+   * whole 256-column tiles and K a multiple of 128.  Not in the reference
+   * (an fp8-activation variant of the FFN). */
+  int a_dtype; const float* a_scale;
 } wam_linear_args;
 
 int wam_linear(const wam_linear_args* args, void* stream);

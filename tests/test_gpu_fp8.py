@@ -139,3 +139,46 @@ def test_block_with_fp8_ffn(dev):
     ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
     m = assert_close(out.cpu(), ref, 0.25, 0.9999, "block fp8 FFN vs bf16-weight oracle")
     print("block fp8 FFN", m)
+
+
+# fp8 activations on the fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4): the
+# activations are quantized per row like the weights (absmax / 448).  Against
+# an fp32 product of the same dequantized operands the only differences are
+# the accumulation order and the output rounding: the bf16 ulp bound.  Against
+# the original bf16 operands, the e4m3 rounding of both (about 2^-5 relative
+# RMS each, so about 3% per output) is the bound's dominant term: relative L2
+# <= 5e-2, cosine >= 0.998 (a single row has only N outputs to average over).
+@pytest.mark.parametrize("M,K,N", [(4680, 3072, 14336), (300, 256, 512), (4680, 128, 256), (1, 3072, 256)])
+def test_fp8_activations_linear(dev, M, K, N):
+    from wam_ops import ops
+    print(f"fp8 x fp8 linear {M}x{K}x{N}", flush=True)
+    x = _randn((M, K), dev, 21)
+    w = _randn((N, K), dev, 22, 0.02)
+    b = _randn((N,), dev, 23, 0.02)
+    qw, sw = ops.quantize_fp8_rows(w)
+    qx, sx = ops.quantize_fp8_rows(x)
+    xd = ofp8.dequantize_rows(qx.cpu(), sx.cpu()).to(dev)
+    wd = ofp8.dequantize_rows(qw.cpu(), sw.cpu()).to(dev)
+    ref = xd @ wd.t() + b.float()
+    y = ops.linear(qx, qw, b, w_scale=sw, x_scale=sx)
+    assert_close(y, ref, _ulp_bound(ref), 0.99999, f"fp8 x fp8 bias {M}x{K}x{N}")
+    y = ops.linear(qx, qw, b, w_scale=sw, x_scale=sx, epilogue=ops.EPI_BIAS_GELU)
+    g = torch.nn.functional.gelu(ref, approximate="tanh")
+    assert_close(y, g, _ulp_bound(g), 0.99999, f"fp8 x fp8 gelu {M}x{K}x{N}")
+    full = x.float() @ w.float().t() + b.float()
+    m = compare(ops.linear(qx, qw, b, w_scale=sw, x_scale=sx), full)
+    print(f"fp8 x fp8 vs bf16 operands: {m}")
+    assert m["rel_l2"] <= 5e-2 and m["cosine"] >= 0.998, m
+
+
+def test_fp8_activations_rejected_without_fp8_weights(dev):
+    from wam_ops import ops
+    x = _randn((64, 256), dev, 1)
+    w = _randn((256, 256), dev, 2, 0.02)
+    qx, sx = ops.quantize_fp8_rows(x)
+    with pytest.raises(RuntimeError):
+        ops.linear(qx, w, None, x_scale=sx)
+    qw, sw = ops.quantize_fp8_rows(w)
+    with pytest.raises(RuntimeError, match="fp8 activations"):
+        ops.linear(qx, qw, None, w_scale=sw, x_scale=sx, epilogue=ops.EPI_BIAS_RES,
+                   residual=torch.zeros(64, 256, device=dev))

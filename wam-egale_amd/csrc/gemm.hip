@@ -41,6 +41,9 @@ struct LinearParams {
   // outputs are multiplied by, and the RoPE table (nfreq, or none).
   float* ssq[3]; const bf16* ngamma[3];
   const float2* nfreq; int nfreq_batch, ntokens, nhd, ssq_ld;
+  // fp8 e4m3 activations (the fp8 MFMA mode): A is [M, K] bytes with one
+  // fp32 scale per row
+  const float* ascale;
 };
 
 constexpr int kEpiPartial = 100;   // kernel epilogue of a split-K range: raw fp32 sums
@@ -542,14 +545,22 @@ struct CfgW4t224f8 {
 // The NM MFMAs of one 16-deep sub-step with the NR fragment reads of the
 // next sub-step, W LDS writes and V global loads spread evenly between them
 // (NM = 16, NR = 8: one read after every second MFMA).
+// (Counts above NM put two of a kind after some MFMAs.)
+template <int MASK>
+__device__ __forceinline__ void sched_n(int c) {
+  if (c == 1) __builtin_amdgcn_sched_group_barrier(MASK, 1, 0);
+  else if (c == 2) __builtin_amdgcn_sched_group_barrier(MASK, 2, 0);
+  else if (c >= 3) __builtin_amdgcn_sched_group_barrier(MASK, 3, 0);
+}
 template <int W, int V, int NM, int NR>
 __device__ __forceinline__ void w4_sched() {
+  static_assert(NR <= 3 * NM && W <= 3 * NM && V <= 3 * NM, "at most 3 of a kind per MFMA");
 #pragma unroll
   for (int q = 0; q < NM; ++q) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     // MFMA
-    if ((q * NR) / NM != ((q + 1) * NR) / NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    if ((q * W) / NM != ((q + 1) * W) / NM) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);    // DS write
-    if ((q * V) / NM != ((q + 1) * V) / NM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+    sched_n<0x100>(((q + 1) * NR) / NM - (q * NR) / NM);    // DS read
+    sched_n<0x200>(((q + 1) * W) / NM - (q * W) / NM);      // DS write
+    sched_n<0x020>(((q + 1) * V) / NM - (q * V) / NM);      // VMEM read
   }
 }
 
@@ -561,17 +572,26 @@ __device__ __forceinline__ void w4_sched() {
 // of them (a quarter row) and widens them exactly to bf16 in registers as it
 // writes the stage, so the LDS layout and the MFMA loop are those of bf16;
 // the scale multiplies the fp32 sums in the epilogue.
-template <int EPI, int RF32, int OF32, int TM, int WB = 2>
+// F8MM: A and W are both e4m3 (per-row and per-column fp32 scales) and the
+// product runs on v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales.  A
+// k-step is then 128 values = 128 bytes per row, so staging, LDS layout and
+// epilogue are those of bf16 byte for byte; only the fragment reads (32 bytes
+// per lane) and the MFMA differ.
+template <int EPI, int RF32, int OF32, int TM, int WB = 2, bool F8MM = false>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   static_assert(TM == 256 || TM == 224, "tile rows");
   static_assert(WB == 2 || WB == 1, "weight bytes");
+  static_assert(!F8MM || (WB == 2 && TM == 224 && (EPI == WAM_EPI_BIAS || EPI == WAM_EPI_BIAS_GELU)),
+                "fp8 MFMA: 224-row tiles, bias or GELU epilogue");
+  constexpr int AE = F8MM ? 1 : 2;        // bytes per A element
+  constexpr int WE = F8MM ? 1 : WB;       // bytes per W element
   constexpr int MB = TM == 256 ? 4 : 7;   // 32-row m-blocks per wave
   constexpr int NB = TM == 256 ? 4 : 2;   // 32-column n-blocks per wave
   constexpr int WGN = TM == 256 ? 2 : 4;  // waves along n
   constexpr int LA = TM / 32;             // A staging loads per thread and k-step
   constexpr int LW = WB == 2 ? 8 : 4;     // W staging loads per thread and k-step
   constexpr int NL = LA + LW;
-  constexpr int WKB = 64 * WB;            // bytes of a weight row per k-step
+  constexpr int WKB = F8MM ? 128 : 64 * WB;  // bytes of a weight row per k-step
   constexpr int NM = MB * NB, NR = MB + NB;  // MFMAs and fragment reads per sub-step
   __shared__ __attribute__((aligned(1024))) char L0[65536];
   __shared__ __attribute__((aligned(1024))) char L1[65536];
@@ -599,7 +619,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   const int n0 = (tn - seg * p.n_tiles_per_seg) * 256;
   const int m0 = tm * TM;
 
-  int nk = p.K / 64, kb = 0;
+  int nk = p.K / (F8MM ? 128 : 64), kb = 0;
   if constexpr (EPI == kEpiPartial) {
     kb = (int)((int64_t)kp * nk / p.k_split);
     nk = (int)((int64_t)(kp + 1) * nk / p.k_split) - kb;
@@ -607,11 +627,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   // Buffer resources that move to k-tile kt: rows past M (A) or past the
   // segment's N (W) load as zeros through the bound.
   const char* wseg = static_cast<const char*>(seg == 0 ? p.w[0] : (seg == 1 ? p.w[1] : p.w[2]));
-  const char* abase = reinterpret_cast<const char*>(p.a + (int64_t)m0 * p.lda) + kb * 128;
-  const char* bbase = wseg + (int64_t)n0 * p.ldw * WB + kb * WKB;
-  const uint32_t abytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * 2u - (uint32_t)kb * 128u;
+  const char* abase = reinterpret_cast<const char*>(p.a) + (int64_t)m0 * p.lda * AE + kb * 128;
+  const char* bbase = wseg + (int64_t)n0 * p.ldw * WE + kb * WKB;
+  const uint32_t abytes = (uint32_t)(p.M - m0) * (uint32_t)p.lda * (uint32_t)AE - (uint32_t)kb * 128u;
   const uint32_t bbytes =
-      (uint32_t)min(256, p.seg_n - n0) * (uint32_t)p.ldw * (uint32_t)WB - (uint32_t)kb * (uint32_t)WKB;
+      (uint32_t)min(256, p.seg_n - n0) * (uint32_t)p.ldw * (uint32_t)WE - (uint32_t)kb * (uint32_t)WKB;
   auto res_a = [&](int kt) { return make_rsrc(abase + kt * 128, abytes - (uint32_t)kt * 128u); };
   auto res_b = [&](int kt) { return make_rsrc(bbase + kt * WKB, bbytes - (uint32_t)kt * (uint32_t)WKB); };
 
@@ -621,9 +641,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   // fp8 weights: W load j is row 64 j + tid / 4, bytes 16 (tid % 4) .. +16,
   // i.e. the bf16 chunks 2 (tid % 4) and 2 (tid % 4) + 1 of that row.
   const int lr = tid >> 3, lc = tid & 7;
-  const int va = lr * (int)p.lda * 2 + lc * 16;
-  const int vb = WB == 2 ? lr * (int)p.ldw * 2 + lc * 16 : (tid >> 2) * (int)p.ldw + (tid & 3) * 16;
-  const int ra32 = 32 * (int)p.lda * 2, rb32 = (WB == 2 ? 32 : 64) * (int)p.ldw * WB;
+  const int va = lr * (int)p.lda * AE + lc * 16;
+  const int vb = WB == 2 ? lr * (int)p.ldw * WE + lc * 16 : (tid >> 2) * (int)p.ldw + (tid & 3) * 16;
+  const int ra32 = 32 * (int)p.lda * AE, rb32 = (WB == 2 ? 32 : 64) * (int)p.ldw * WE;
   const int wofs = lds_off<8>(lr, lc);
   const int wofs8_0 = lds_off<8>(tid >> 2, 2 * (tid & 3)), wofs8_1 = lds_off<8>(tid >> 2, 2 * (tid & 3) + 1);
   typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
@@ -668,6 +688,65 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[j][i] = f32x16{};
+  if constexpr (F8MM) {
+  // fp8 MFMA k loop.  One staging set (k-step t+1 written to the free stage
+  // and reloaded with t+2 during step t: one step of lead) and two sub-steps
+  // of 64 values per 128-byte k-step; a lane's fragment is 32 bytes of its
+  // row at logical chunks 4 s + 2 half and 4 s + 2 half + 1.
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  i32x8 ga[2][MB], gb[2][NB];
+  const int rowa = (wm * 32 * MB + l32) * 128, rowb = 32768 + (wn * 32 * NB + l32) * 128;
+  auto frag8 = [&](const char* p8, int s) {
+    const int sw = (l32 >> 1) & 7, c = 4 * s + 2 * half;
+    const u32x4s lo = *reinterpret_cast<const u32x4s*>(p8 + ((c ^ sw) << 4));
+    const u32x4s hi = *reinterpret_cast<const u32x4s*>(p8 + (((c + 1) ^ sw) << 4));
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  auto rd8 = [&](const char* buf, int s, int f) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) ga[f][i] = frag8(buf + rowa + i * 4096, s);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) gb[f][j] = frag8(buf + rowb + j * 4096, s);
+  };
+  auto mm8 = [&](int f) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(gb[f][j], ga[f][i], acc[j][i], 0, 0, 0, 127,
+                                                                    0, 127);
+  };
+  // Prologue: k-step 0 into L0, k-step 1 into the staging set.
+  gload(S0, 0, I0{}, INL{});
+  swrite(S0, L0, I0{}, INL{});
+  gload(S0, min(1, nk - 1), I0{}, INL{});
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  rd8(L0, 0, 0);
+  // Step t: sub-step 0 from `cur` with the writes of k-step t+1 to `nxt` and
+  // the loads of k-step t+2; the barrier; sub-step 1 with the reads of the
+  // next step's sub-step 0 from `nxt`.
+  auto kstep8 = [&](int t, char* cur, char* nxt) {
+    rd8(cur, 1, 1);
+    swrite(S0, nxt, I0{}, INL{});
+    gload(S0, min(t + 2, nk - 1), I0{}, INL{});
+    mm8(0);
+    w4_sched<NL, NL, NM, NR * 2>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    rd8(nxt, 0, 0);
+    mm8(1);
+    w4_sched<0, 0, NM, NR * 2>();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
+    kstep8(t, L0, L1);
+    kstep8(t + 1, L1, L0);
+  }
+  if (t < nk) kstep8(t, L0, L1);
+  } else {
   // Fragments of a sub-step: rows wm*32*MB + 32 i + l32 of A and wn*32*NB +
   // 32 j + l32 of W at logical chunk 2 s + half; the swizzle term is
   // (l32 >> 1) & 7.
@@ -739,6 +818,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     kstep(t + 1, L1, L0, S0);
   }
   if (t < nk) kstep(t, L0, L1, S1);
+  }
 
   // ------------------------------------------------------------- epilogue
   // Two rounds of 128 rows through both stage buffers (1 KB fp32 rows, 16-byte
@@ -762,7 +842,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     }
   }
   float wsc[4] = {1.f, 1.f, 1.f, 1.f};  // fp8 weight scales of the lane's columns
-  if constexpr (WB == 1 && EPI != kEpiPartial) {
+  if constexpr ((WB == 1 || F8MM) && EPI != kEpiPartial) {
     const float4 t = *reinterpret_cast<const float4*>((seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2])) + n);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
@@ -929,8 +1009,15 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           continue;
         }
         float y[4];
+        if constexpr (F8MM) {
+          // row scale of the fp8 activations times the column scale
+          const float sr = p.ascale[min(m0 + row, p.M - 1)];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? vv[k8][e] * wsc[e] + bv[e] : vv[k8][e] + bv[e];
+          for (int e = 0; e < 4; ++e) y[e] = vv[k8][e] * (sr * wsc[e]) + bv[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = WB == 1 ? vv[k8][e] * wsc[e] + bv[e] : vv[k8][e] + bv[e];
+        }
         if constexpr (EPI == WAM_EPI_BIAS_GELU) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
@@ -1324,9 +1411,11 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a->seg_n % 8 == 0 && (a->n_seg == 1 || a->seg_n % 128 == 0),
               "wam_linear: N=%d must be a multiple of 8 (of 128 with several segments)", a->seg_n);
   WAM_REQUIRE(a->w_dtype == WAM_BF16 || a->w_dtype == WAM_FP8, "wam_linear: w_dtype %d", a->w_dtype);
+  WAM_REQUIRE(a->a_dtype == WAM_BF16 || a->a_dtype == WAM_FP8, "wam_linear: a_dtype %d", a->a_dtype);
   const bool f8 = a->w_dtype == WAM_FP8;
+  const bool a8 = a->a_dtype == WAM_FP8;
   const int wb = f8 ? 1 : 2;
-  WAM_REQUIRE(a->lda % 8 == 0 && (a->ldw * wb) % 16 == 0 && a->ldo % 4 == 0,
+  WAM_REQUIRE((a->lda * (a8 ? 1 : 2)) % 16 == 0 && (a->ldw * wb) % 16 == 0 && a->ldo % 4 == 0,
               "wam_linear: row strides must keep 16-byte alignment");
   WAM_REQUIRE(a->a != nullptr, "wam_linear: null activation");
   WAM_REQUIRE((int64_t)a->M * a->lda * 2 < (int64_t)1 << 31 && (int64_t)a->seg_n * a->ldw * wb < (int64_t)1 << 31,
@@ -1396,6 +1485,25 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     p.ssq_ld = (a->seg_n + 255) / 256;
   }
   const bool big = uses_big_tiles(a->M, a->seg_n, a->n_seg);
+  if (a8) {
+    WAM_REQUIRE(f8 && a->a_scale != nullptr, "wam_linear: fp8 activations need fp8 weights and a_scale");
+    WAM_REQUIRE((a->epilogue == WAM_EPI_BIAS || a->epilogue == WAM_EPI_BIAS_GELU) && !norm,
+                "wam_linear: fp8 activations take WAM_EPI_BIAS or WAM_EPI_BIAS_GELU");
+    WAM_REQUIRE(a->n_seg == 1 && a->seg_n % 256 == 0 && a->K % 128 == 0,
+                "wam_linear: fp8 activations need one segment, N a multiple of 256 and K of 128 (N=%d K=%d)",
+                a->seg_n, a->K);
+    p.ascale = a->a_scale;
+    p.n_tiles_per_seg = a->seg_n / 256;
+    p.m_tiles = (a->M + 223) / 224;
+    p.n_tiles = p.n_tiles_per_seg;
+    const dim3 grid((unsigned)(p.m_tiles * p.n_tiles));
+    if (a->epilogue == WAM_EPI_BIAS)
+      hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GELU, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
+    WAM_LAUNCHED("gemm_w4_kernel (fp8 MFMA)");
+    return WAM_OK;
+  }
   if (f8) {
     // fp8 weights: the four-wave kernel widens them to bf16 as it stages
     // them (FFN unit at 4680 rows, alternating runs on one box: 713-714 us

@@ -46,7 +46,8 @@ class LinearArgs(Structure):
                 ("w_dtype", c_int), ("w_scale", c_void_p * 3),
                 ("workspace", c_void_p), ("workspace_bytes", c_int64),
                 ("norm_ssq", c_void_p * 3), ("norm_gamma", c_void_p * 3), ("norm_freq", c_void_p),
-                ("norm_freq_batch", c_int), ("norm_tokens", c_int), ("norm_head_dim", c_int)]
+                ("norm_freq_batch", c_int), ("norm_tokens", c_int), ("norm_head_dim", c_int),
+                ("a_dtype", c_int), ("a_scale", c_void_p)]
 
 
 class LnArgs(Structure):

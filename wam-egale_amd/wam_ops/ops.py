@@ -104,7 +104,7 @@ def quantize_fp8_rows(w, out=None, scale=None):
 
 def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=None,
            temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16, w_scale=None,
-           norm_gamma=None, norm_freq=None, norm_head_dim=128):
+           norm_gamma=None, norm_freq=None, norm_head_dim=128, x_scale=None):
     """Y = epilogue(x W^T + b) on MFMA.  weights: one tensor or a list of up to 3
     (one launch, outputs split per weight).  Returns a tensor or a list.
     The residual may be bf16 or fp32; out_dtype=float32 is allowed for the
@@ -117,7 +117,12 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
     y = bf16(x W^T + b), rotated by norm_freq (complex64 [Bf, tokens, 1 or
     absent, head_dim / 2], or None), and the call returns (outputs, sums)
     where sums[i] is the fp32 [M, ceil(N / 256)] sum of y^2 per row and
-    256-column group (None for segments without a gamma)."""
+    256-column group (None for segments without a gamma).
+
+    x may be float8_e4m3fn with x_scale, fp32 [M] per-row scales (from
+    quantize_fp8_rows), when the weights are fp8 too: the product then runs
+    on the fp8 MFMA, y = acc * x_scale[m] * w_scale[n] + b (bias or GELU
+    epilogue, one weight, N a multiple of 256, K of 128)."""
     single = torch.is_tensor(weights)
     ws = [weights] if single else list(weights)
     bs = [biases] if (single or biases is None) else list(biases)
@@ -132,8 +137,14 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         _req(len(scs) == len(ws), "one w_scale per weight")
     else:
         _req(w_scale is None, "w_scale is only for fp8 weights")
-    dev = _dev(x, *ws, *[b for b in bs if b is not None], residual, *scs)
-    _bf16(x, "x")
+    dev = _dev(x, *ws, *[b for b in bs if b is not None], residual, *scs, x_scale)
+    x8 = x.dtype == FP8
+    if x8:
+        _req(f8 and x_scale is not None and x_scale.dtype == torch.float32 and x_scale.is_contiguous(),
+             "fp8 activations need fp8 weights and fp32 x_scale [M]")
+    else:
+        _req(x_scale is None, "x_scale is only for fp8 activations")
+        _bf16(x, "x")
     _req(x.dim() >= 2 and x.stride(-1) == 1, "x must have a contiguous last dim")
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
@@ -169,6 +180,9 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         for i, sc in enumerate(scs):
             a.w_scale[i] = sc.data_ptr()
     a.out_dtype = dtype_code(outs[0])
+    if x8:
+        _req(x_scale.numel() == M, "x_scale must be [M]")
+        a.a_dtype, a.a_scale = _lib.WAM_FP8, x_scale.data_ptr()
     ssqs = None
     if norm_gamma is not None:
         gs = [norm_gamma] if torch.is_tensor(norm_gamma) else list(norm_gamma)
