@@ -467,26 +467,37 @@ def main():
         "C4b_cross_attention": _unit(stages["cross_attn"], 4 * M * Lc * D),
         "C4a_self_attention": c4a_attention(shape, dev, args.steps, args.warmup),
     }
-    # C3 second variant: the same layer with e4m3 FFN weights (per-output-channel
-    # fp32 scales, bf16 activations); everything else unchanged.
-    flayer = WholeLayerBlock(blk, ffn_fp8=True)
-    with torch.no_grad():
-        flayer.prepare_context(ctx, precompute=True)
-
-    def fstep(timer=None):
-        with torch.no_grad():
-            return flayer(x, ctx, temb, freqs, timer=timer)
-    fms = timed_steps(fstep, args.steps, args.warmup, gate="L4680 fp8 FFN")
-    fst = stage_times(lib, fstep, 3, (1 << len(_lib.STAGES)) - 1)
+    # C3 variants: the same layer with e4m3 FFN weights (per-output-channel
+    # fp32 scales) and bf16 activations, and with FFN1's input quantized too
+    # (per-row scales, inside LayerNorm 3; FFN1 on the fp8 MFMA); everything
+    # else unchanged.
     ffn_flops = 2 * 2 * M * D * F
-    out["fp8_ffn_variant"] = {
-        "us_per_layer": round(fms * 1e3, 1), "tokens_per_s": round(M / (fms * 1e-3), 1),
-        "ffn_unit_us": round((fst["ffn1"] + fst["ffn2"]) * 1e3, 1),
-        "ffn_unit_us_bf16": round((stages["ffn1"] + stages["ffn2"]) * 1e3, 1),
-        "ffn_unit_tflops": round(ffn_flops / ((fst["ffn1"] + fst["ffn2"]) * 1e-3) / 1e12, 1),
-        "weights": "e4m3 per-output-channel scales (absmax/448), bf16 activations, fp32 accumulate",
+    variants = {
+        "fp8_ffn_variant": (dict(ffn_fp8=True),
+                            "e4m3 per-output-channel scales (absmax/448), bf16 activations, fp32 accumulate"),
+        "fp8_act_ffn_variant": (dict(ffn_fp8=True, ffn_act_fp8=True),
+                                "e4m3 weights as above; FFN1 input e4m3 with per-row scales (absmax/448, "
+                                "written by LayerNorm 3) on the fp8 MFMA; FFN2 bf16 activations"),
     }
-    del flayer
+    for key, (opts, what) in variants.items():
+        flayer = WholeLayerBlock(blk, **opts)
+        with torch.no_grad():
+            flayer.prepare_context(ctx, precompute=True)
+
+        def fstep(timer=None):
+            with torch.no_grad():
+                return flayer(x, ctx, temb, freqs, timer=timer)
+        fms = timed_steps(fstep, args.steps, args.warmup, gate=f"L4680 {key}")
+        fst = stage_times(lib, fstep, 3, (1 << len(_lib.STAGES)) - 1)
+        out[key] = {
+            "us_per_layer": round(fms * 1e3, 1), "tokens_per_s": round(M / (fms * 1e-3), 1),
+            "ffn_unit_us": round((fst["ffn1"] + fst["ffn2"]) * 1e3, 1),
+            "ffn1_us": round(fst["ffn1"] * 1e3, 1), "ln3_us": round(fst["ln3"] * 1e3, 1),
+            "ffn_unit_us_bf16": round((stages["ffn1"] + stages["ffn2"]) * 1e3, 1),
+            "ffn_unit_tflops": round(ffn_flops / ((fst["ffn1"] + fst["ffn2"]) * 1e-3) / 1e12, 1),
+            "weights": what,
+        }
+        del flayer
     if not args.no_verify:
         # Lverify: 4 candidates x 1560 tokens, each over the shared 6240-token
         # prefix (pool row 0) plus its own 1560 tokens; read-only cache.

@@ -187,6 +187,13 @@ typedef struct {
   int affine;
   const void* gamma; const void* beta; int gb_dtype; /* affine == 1 */
   wam_modulation mod; int shift_index;              /* affine == 0 */
+  /* Optional e4m3 copy of y (no counterpart in the reference; the fp8
+   * activations of wam_linear): y8 [rows, D] bytes and y8_scale [rows] fp32
+   * with y8_scale[r] = max_d |y[r,d]| / 448 (1 for an all-zero row) and
+   * y8[r,d] = e4m3(y[r,d] / y8_scale[r]) rounded to nearest even, y being the
+   * bf16 result (the same bytes wam_quantize_fp8_rows makes of it).  With y8
+   * set, y may be NULL (no bf16 output). */
+  void* y8; float* y8_scale;
 } wam_ln_args;
 
 int wam_ln_modulate(const wam_ln_args* args, void* stream);
@@ -312,6 +319,12 @@ typedef struct {
    * (wam_quantize_fp8_rows of w[23] and w[25]); the biases stay w[24], w[26]. */
   const void* ffn_fp8[2];
   const float* ffn_scale[2];
+  /* With ffn_fp8 set: ffn_act_fp8 = 1 also quantizes FFN1's input per row
+   * (LayerNorm 3 writes e4m3 rows with absmax/448 scales, as wam_ln_args.y8)
+   * and runs FFN1 on the fp8 MFMA (wam_linear a_dtype = WAM_FP8).  Needs
+   * ffn_dim to be a multiple of 256.  Workspace: the layout always holds the
+   * e4m3 rows and their scales. */
+  int ffn_act_fp8;
 } wam_block_weights;
 
 #define WAM_DEBUG_SLOTS 28

@@ -123,6 +123,11 @@ def test_block_host_validation():
         w.w[i] = 256 * (i + 1)
     w.dim = 300
     assert "must equal heads" in _err(h.wam_block_forward(ctypes.byref(args), None))
+    w.dim, w.ffn_act_fp8 = 256, 1  # fp8 activations without the fp8 weights
+    assert "fp8 FFN activations" in _err(h.wam_block_forward(ctypes.byref(args), None))
+    w.ffn_fp8[0] = w.ffn_fp8[1] = w.ffn_scale[0] = w.ffn_scale[1] = 16
+    w.ffn_dim = 384  # not whole 256-column tiles
+    assert "ffn_dim % 256" in _err(h.wam_block_forward(ctypes.byref(args), None))
 
 
 def test_workspace_size():
@@ -130,6 +135,7 @@ def test_workspace_size():
     R, D, F, Lc = 4680, 3072, 14336, 512
     n = h.wam_block_workspace_bytes(1, R, D, F, 1, Lc, 0)
     expect = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
+              + R * D + R * 4  # e4m3 copy of the LayerNorm-3 rows and their scales
               + R * 4  # new-slot list
               + R * (D // 256) * 4  # per-row query sums of squares per 256-column group
               + (1 + 2) * D * 4)  # zero modulation for the unmodulated LayerNorm debug outputs
@@ -167,7 +173,8 @@ def test_attention_split_plan_workspace():
     # the block reserves one region for the largest of its split needs
     B, M, D, F, Lc, P = 4, 1560, 3072, 14336, 512, 7800
     R = B * M
-    core = (R * D * 2 + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
+    core = (R * D * 2 + R * D + R * 4  # LayerNorm rows, their e4m3 copy and its scales
+            + R * 3 * D * 2 + R * D * 2 + 2 * R * D * 4 + 2 * Lc * D * 2 + R * F * 2
             + P * 4 + M * 4  # slot lists
             + R * (D // 256) * 4  # query sums of squares
             + (B + 2) * D * 4)  # zero modulation (debug LayerNorms)
@@ -192,6 +199,8 @@ def test_modulation_host_validation():
     assert "shift index" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
     a.mod.tokens = 5
     assert "divisible by tokens" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
+    a.mod.tokens, a.shift_index, a.y8 = 6, 0, 16  # e4m3 rows without their scales
+    assert "y8_scale" in _err(h.wam_ln_modulate(ctypes.byref(a), None))
 
 
 def test_model_io_host_validation():

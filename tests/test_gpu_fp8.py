@@ -182,3 +182,71 @@ def test_fp8_activations_rejected_without_fp8_weights(dev):
     with pytest.raises(RuntimeError, match="fp8 activations"):
         ops.linear(qx, qw, None, w_scale=sw, x_scale=sx, epilogue=ops.EPI_BIAS_RES,
                    residual=torch.zeros(64, 256, device=dev))
+
+
+# LayerNorm 3 with e4m3 rows: the fused quantization equals the row quantizer
+# applied to the kernel's own bf16 output, byte for byte (and the oracle's
+# quantization of it), for every row-chunk count of the kernel (D 128, 1024,
+# 3072, 4096), fp32 and bf16 inputs, a row count that leaves a partial
+# workgroup, per-token modulation, and an all-zero output row (scale 1).
+@pytest.mark.parametrize("D", [128, 1024, 3072, 4096])
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+def test_ln_modulate_fp8_rows(dev, D, xdtype):
+    from wam_ops import ops
+    B, M = 2, 13
+    g = torch.Generator(device=dev).manual_seed(D)
+    x = (torch.randn(B, M, D, generator=g, device=dev) * 3).to(xdtype)
+    table = torch.randn(1, 6, D, generator=g, device=dev) * 0.1
+    temb = torch.randn(B, M, 6, D, generator=g, device=dev) * 0.1
+    x[1, 4] = 1.5            # constant row: LN gives 0 ...
+    table[0, 3] = 0
+    temb[1, 4, 3] = 0        # ... and a zero shift keeps it 0
+    y, q, sc = ops.ln_modulate(x, table, temb, 3, fp8=True)
+    y_only = ops.ln_modulate(x, table, temb, 3)
+    _, q2, sc2 = ops.ln_modulate(x, table, temb, 3, fp8=True, bf16_out=False)
+    qr, sr = ops.quantize_fp8_rows(y_only.reshape(B * M, D))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_only)
+    assert torch.equal(q.view(torch.uint8).reshape(B * M, D), qr.view(torch.uint8))
+    assert torch.equal(sc, sr)
+    assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(sc2, sc)
+    assert sc[B * M - M + 4].item() == 1.0 and not q.view(torch.uint8)[1, 4].any()
+    qo, so = ofp8.quantize_rows(y_only.reshape(B * M, D).cpu())
+    assert torch.equal(sc.cpu(), so) and torch.equal(q.cpu().view(torch.uint8).reshape(B * M, D), qo.view(torch.uint8))
+
+
+def test_block_with_fp8_ffn_activations(dev):
+    """The block with e4m3 FFN weights and e4m3 FFN1 activations (quantized
+    per row inside LayerNorm 3).  FFN1 before GELU against the fp32 product of
+    the oracle's quantization of the block's own LayerNorm-3 rows and the
+    dequantized weight: the bf16 ulp bound (only the accumulation order and
+    the output rounding differ).  The output against the bf16-weight oracle
+    at the fp8 bound; a debug call leaves the output unchanged."""
+    from oracle.block import block_forward
+    from wam_ops import synthetic
+    from wam_ops.block import TransformerBlock
+    from wam_ops.whole_layer import WholeLayerBlock
+    shape = synthetic.BlockShape(3072, 24, 14336)
+    params = synthetic.block_params(shape, seed=21)
+    x, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 4 * 8 * 8, (4, 8, 8), context_len=512, seed=22)
+    blk = TransformerBlock(shape.dim, shape.ffn, shape.heads, cross_attn_norm=True, eps=shape.eps)
+    with torch.no_grad():
+        for name, prm in blk.named_parameters():
+            prm.data = params[name].to(dev)
+    wl = WholeLayerBlock(blk.to(dev), ffn_fp8=True, ffn_act_fp8=True)
+    with torch.no_grad():
+        wl.prepare_context(ctx.to(dev), precompute=True)
+        out = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
+        dbg = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), debug=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dbg["output"], out), "a debug call changed the block output"
+    q1, s1, _, _ = wl.bound().ffn_fp8
+    h = dbg["modulated3"].reshape(-1, shape.dim).cpu()
+    qh, sh = ofp8.quantize_rows(h)
+    ffn1 = ofp8.dequantize_rows(qh, sh) @ ofp8.dequantize_rows(q1.cpu(), s1.cpu()).t() \
+        + params["ffn.net.0.proj.bias"].float()
+    got = dbg["ffn1"].reshape(ffn1.shape).cpu()
+    assert_close(got, ffn1, _ulp_bound(ffn1), 0.99999, "block fp8 FFN1 (fp8 activations)")
+    ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
+    m = assert_close(out.cpu(), ref, 0.5, 0.9995, "block fp8 FFN activations vs bf16-weight oracle")
+    print("block fp8 FFN activations", m)

@@ -73,7 +73,7 @@ struct Scope {
 static size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
 
 struct Layout {
-  size_t h, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, ssq, zeros, split, split_bytes, total;
+  size_t h, h8, h8s, qkv, attn, x1, x2, ck, cv, act, slots, newslots, info, ssq, zeros, split, split_bytes, total;
 };
 
 static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
@@ -82,6 +82,9 @@ static Layout layout(int B, int M, int D, int F, int Bc, int Lc, int pool) {
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
   L.h = take(R * D * 2);
+  // e4m3 rows of the LayerNorm-3 output and their scales (fp8 FFN1 input).
+  L.h8 = take(R * D);
+  L.h8s = take(R * 4);
   L.qkv = take(R * 3 * D * 2);
   L.attn = take(R * D * 2);
   L.x1 = take(R * D * 4);  // residual stream kept in fp32
@@ -164,6 +167,9 @@ static int check_weights(const wam_block_weights* w) {
   WAM_REQUIRE(w->norm2_dtype == WAM_F32 || w->norm2_dtype == WAM_BF16, "block: norm2 dtype");
   WAM_REQUIRE(!w->ffn_fp8[0] || (w->ffn_fp8[1] && w->ffn_scale[0] && w->ffn_scale[1]),
               "block: fp8 FFN needs both weights and both scale vectors");
+  WAM_REQUIRE(!w->ffn_act_fp8 || (w->ffn_fp8[0] && w->ffn_dim % 256 == 0),
+              "block: fp8 FFN activations need the fp8 FFN weights and ffn_dim %% 256 == 0 (ffn_dim=%d)",
+              w->ffn_dim);
   return WAM_OK;
 }
 
@@ -228,6 +234,8 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   void* split_ws = L.split_bytes ? ws + L.split : nullptr;
   const int64_t split_bytes = (int64_t)L.split_bytes;
   bf16* h = reinterpret_cast<bf16*>(ws + L.h);
+  uint8_t* h8 = reinterpret_cast<uint8_t*>(ws + L.h8);
+  float* h8s = reinterpret_cast<float*>(ws + L.h8s);
   bf16* qkv = reinterpret_cast<bf16*>(ws + L.qkv);
   bf16* attn = reinterpret_cast<bf16*>(ws + L.attn);
   float* x1 = reinterpret_cast<float*>(ws + L.x1);
@@ -280,6 +288,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     gemm_args(g, x, K, R, K, N, W->w[wi], W->w[wi + 1], y, N);
     if (wf8 >= 0 && W->ffn_fp8[0]) {
       g.w[0] = W->ffn_fp8[wf8]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[wf8];
+    }
+    if (wf8 == 0 && W->ffn_act_fp8) {
+      g.a = h8; g.a_dtype = WAM_FP8; g.a_scale = h8s;  // the fused FFN1's own input
     }
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     return linear(&g, s);
@@ -482,6 +493,11 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     wam_ln_args l{};
     l.x = x2; l.x_dtype = WAM_F32; l.y = h; l.rows = R; l.D = D; l.eps = W->eps[2]; l.affine = 0;
     l.mod = mod; l.shift_index = 3;
+    if (W->ffn_act_fp8) {
+      // e4m3 rows for the fp8 FFN1; the bf16 rows only when a debug copy reads them
+      l.y8 = h8; l.y8_scale = h8s;
+      if (!dbg(12)) l.y = nullptr;
+    }
     WAM_TRY(ln_modulate(&l, s));
   }
   WAM_TRY(copy_debug(a->debug, 12, h, rowb, s));
@@ -494,6 +510,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.epilogue = WAM_EPI_BIAS_GELU;
     if (W->ffn_fp8[0]) {
       g.w[0] = W->ffn_fp8[0]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[0];
+    }
+    if (W->ffn_act_fp8) {
+      g.a = h8; g.a_dtype = WAM_FP8; g.a_scale = h8s;
     }
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));

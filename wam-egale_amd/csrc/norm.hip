@@ -53,7 +53,11 @@ __device__ inline void ln_coeffs(const wam_ln_args& a, int64_t row, int ch, floa
   }
 }
 
-template <int CH, bool XF32>
+// Q8: the bf16 rows are also written as e4m3 with one fp32 scale per row,
+// scale = max |bf16 row| / 448 (1 for an all-zero row), q = e4m3(y / scale)
+// rounded to nearest even: what the row quantizer of the fp8 GEMM makes of
+// the bf16 output, without reading it back.
+template <int CH, bool XF32, bool Q8>
 __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args a) {
   __shared__ __attribute__((aligned(16))) float s_mul[kLnMaxD];
   __shared__ __attribute__((aligned(16))) float s_add[kLnMaxD];
@@ -94,6 +98,7 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args 
   }
   const float rstd = rsqrtf(wave_sum(q) / D + a.eps);
   bf16* y = static_cast<bf16*>(a.y) + row * D;
+  float mx = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int ch = lane + c * 64;
@@ -114,26 +119,51 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args 
     bf16x8 o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = static_cast<bf16>((v[c][e] - mean) * rstd * mul[e] + add[e]);
-    st_bf16x8(y + ch * 8, o);
+    if (!Q8 || a.y) st_bf16x8(y + ch * 8, o);
+    if (Q8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[c][e] = static_cast<float>(o[e]);
+        mx = fmaxf(mx, fabsf(v[c][e]));
+      }
+    }
+  }
+  if (Q8) {
+    const float amax = wave_max(mx);
+    const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+    uint8_t* q = static_cast<uint8_t*>(a.y8) + row * D;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int ch = lane + c * 64;
+      if (ch >= nch) continue;
+      int lo = 0, hi = 0;
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][0] / sc, v[c][1] / sc, lo, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][2] / sc, v[c][3] / sc, lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][4] / sc, v[c][5] / sc, hi, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][6] / sc, v[c][7] / sc, hi, true);
+      *reinterpret_cast<u32x2*>(q + ch * 8) = u32x2{(unsigned)lo, (unsigned)hi};
+    }
+    if (lane == 0) a.y8_scale[row] = sc;
   }
 }
 
-template <bool XF32>
+template <bool XF32, bool Q8>
 static void launch_ln(const wam_ln_args* a, hipStream_t s) {
   const dim3 grid((unsigned)((a->rows + kLnWaves - 1) / kLnWaves)), block(64 * kLnWaves);
   const int ch = (a->D / 8 + 63) / 64;
-  if (ch <= 1) hipLaunchKernelGGL((ln_modulate_kernel<1, XF32>), grid, block, 0, s, *a);
-  else if (ch <= 2) hipLaunchKernelGGL((ln_modulate_kernel<2, XF32>), grid, block, 0, s, *a);
-  else if (ch <= 3) hipLaunchKernelGGL((ln_modulate_kernel<3, XF32>), grid, block, 0, s, *a);
-  else if (ch <= 6) hipLaunchKernelGGL((ln_modulate_kernel<6, XF32>), grid, block, 0, s, *a);
-  else hipLaunchKernelGGL((ln_modulate_kernel<8, XF32>), grid, block, 0, s, *a);
+  if (ch <= 1) hipLaunchKernelGGL((ln_modulate_kernel<1, XF32, Q8>), grid, block, 0, s, *a);
+  else if (ch <= 2) hipLaunchKernelGGL((ln_modulate_kernel<2, XF32, Q8>), grid, block, 0, s, *a);
+  else if (ch <= 3) hipLaunchKernelGGL((ln_modulate_kernel<3, XF32, Q8>), grid, block, 0, s, *a);
+  else if (ch <= 6) hipLaunchKernelGGL((ln_modulate_kernel<6, XF32, Q8>), grid, block, 0, s, *a);
+  else hipLaunchKernelGGL((ln_modulate_kernel<8, XF32, Q8>), grid, block, 0, s, *a);
 }
 
 int ln_modulate(const wam_ln_args* a, hipStream_t s) {
   WAM_REQUIRE(a != nullptr, "wam_ln_modulate: null args");
   WAM_REQUIRE(a->rows >= 0 && a->D > 0 && a->D % 8 == 0 && a->D <= 4096,
               "wam_ln_modulate: D=%d must be a multiple of 8 and <= 4096", a->D);
-  WAM_REQUIRE(a->x && a->y, "wam_ln_modulate: null x/y");
+  WAM_REQUIRE(a->x && (a->y || a->y8), "wam_ln_modulate: null x/y");
+  WAM_REQUIRE(!a->y8 || a->y8_scale, "wam_ln_modulate: y8 needs y8_scale");
   WAM_REQUIRE(a->x_dtype == WAM_BF16 || a->x_dtype == WAM_F32, "wam_ln_modulate: x dtype");
   if (a->affine) {
     WAM_REQUIRE(a->gamma && a->beta, "wam_ln_modulate: affine needs gamma and beta");
@@ -144,8 +174,9 @@ int ln_modulate(const wam_ln_args* a, hipStream_t s) {
                 a->shift_index);
   }
   if (a->rows == 0) return WAM_OK;
-  if (a->x_dtype == WAM_F32) launch_ln<true>(a, s);
-  else launch_ln<false>(a, s);
+  const bool q8 = a->y8 != nullptr;
+  if (a->x_dtype == WAM_F32) q8 ? launch_ln<true, true>(a, s) : launch_ln<true, false>(a, s);
+  else q8 ? launch_ln<false, true>(a, s) : launch_ln<false, false>(a, s);
   WAM_LAUNCHED("ln_modulate_kernel");
   return WAM_OK;
 }

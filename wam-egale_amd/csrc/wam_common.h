@@ -275,6 +275,19 @@ __device__ inline float wave_sum(float v) {
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
 }
 
+// The same butterfly with max (wave-uniform result).
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  const int i = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48))));
+}
+
 // Eight sums over the 64 lanes of a wave at once: v[k] summed over all lanes
 // lands in out[j] for k = j + 2 (r & 1) + 4 (r >> 1), r = lane / 16, on all
 // 16 lanes of row r.  Two halving exchanges (v_permlane32_swap trades the

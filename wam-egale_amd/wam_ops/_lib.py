@@ -53,7 +53,8 @@ class LinearArgs(Structure):
 class LnArgs(Structure):
     _fields_ = [("x", c_void_p), ("y", c_void_p), ("rows", c_int), ("D", c_int),
                 ("x_dtype", c_int), ("eps", c_float), ("affine", c_int), ("gamma", c_void_p),
-                ("beta", c_void_p), ("gb_dtype", c_int), ("mod", Modulation), ("shift_index", c_int)]
+                ("beta", c_void_p), ("gb_dtype", c_int), ("mod", Modulation), ("shift_index", c_int),
+                ("y8", c_void_p), ("y8_scale", c_void_p)]
 
 
 class RmsRopeArgs(Structure):
@@ -93,7 +94,8 @@ class KvCommitArgs(Structure):
 class BlockWeights(Structure):
     _fields_ = [("w", c_void_p * 27), ("table_dtype", c_int), ("norm2_dtype", c_int),
                 ("dim", c_int), ("heads", c_int), ("head_dim", c_int), ("ffn_dim", c_int),
-                ("eps", c_float * 7), ("ffn_fp8", c_void_p * 2), ("ffn_scale", c_void_p * 2)]
+                ("eps", c_float * 7), ("ffn_fp8", c_void_p * 2), ("ffn_scale", c_void_p * 2),
+                ("ffn_act_fp8", c_int)]
 
 
 class BlockArgs(Structure):

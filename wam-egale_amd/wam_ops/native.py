@@ -48,7 +48,7 @@ def _check(cond, msg):
 class BoundWeights:
     """Validated parameter pointers packed into a wam_block_weights struct."""
 
-    def __init__(self, weights, eps, heads, ffn_fp8=False):
+    def __init__(self, weights, eps, heads, ffn_fp8=False, ffn_act_fp8=False):
         _check(len(weights) == 27 and len(eps) == 7, "native parameter schema: 27 weights, 7 eps")
         dev = weights[3].device
         _check(dev.type == "cuda", "native block parameters must live on the GPU")
@@ -77,6 +77,10 @@ class BoundWeights:
             self.ffn_fp8 = (q1, s1, q2, s2)
             st.ffn_fp8[0], st.ffn_fp8[1] = q1.data_ptr(), q2.data_ptr()
             st.ffn_scale[0], st.ffn_scale[1] = s1.data_ptr(), s2.data_ptr()
+        if ffn_act_fp8:
+            # FFN1 input quantized per row inside LayerNorm 3, FFN1 on the fp8 MFMA
+            _check(ffn_fp8, "fp8 FFN activations need the fp8 FFN weights")
+            st.ffn_act_fp8 = 1
         self.struct = st
 
 

@@ -229,19 +229,30 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
     return res
 
 
-def ln_modulate(x, table, temb, shift_index, eps=1e-6, out=None):
-    """bf16(LN(x) * (1 + mod[shift+1]) + mod[shift]), x [B, M, D] bf16 or fp32."""
+def ln_modulate(x, table, temb, shift_index, eps=1e-6, out=None, fp8=False, bf16_out=True):
+    """bf16(LN(x) * (1 + mod[shift+1]) + mod[shift]), x [B, M, D] bf16 or fp32.
+
+    fp8=True also writes the result as float8_e4m3fn rows with fp32 scales
+    [B * M] (max |row| / 448, as quantize_fp8_rows of the bf16 result) and
+    returns (y, q, scale); bf16_out=False then skips the bf16 output (y None)."""
     dev = _dev(x, table, temb)
     _req(x.dim() == 3 and x.is_contiguous(), "x must be [B, M, D] contiguous")
+    _req(fp8 or bf16_out, "bf16_out=False needs fp8=True")
     B, M, D = x.shape
-    y = out if out is not None else torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    y = None
+    if bf16_out:
+        y = out if out is not None else torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
     a = _lib.LnArgs()
-    a.x, a.y, a.rows, a.D, a.eps, a.affine = x.data_ptr(), y.data_ptr(), B * M, D, eps, 0
+    a.x, a.y, a.rows, a.D, a.eps, a.affine = x.data_ptr(), y.data_ptr() if y is not None else None, B * M, D, eps, 0
     a.x_dtype = dtype_code(x)
     a.mod = modulation(table, temb, M)
     a.shift_index = shift_index
+    if fp8:
+        q = torch.empty(x.shape, dtype=FP8, device=dev)
+        sc = torch.empty(B * M, dtype=torch.float32, device=dev)
+        a.y8, a.y8_scale = q.data_ptr(), sc.data_ptr()
     _lib.check(_lib.lib().wam_ln_modulate(ctypes.byref(a), stream_handle(dev)), "wam_ln_modulate")
-    return y
+    return (y, q, sc) if fp8 else y
 
 
 def layer_norm_affine(x, gamma, beta, eps=1e-6, out=None):

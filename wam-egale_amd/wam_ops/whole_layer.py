@@ -19,11 +19,14 @@ from .ops import stream_handle
 class WholeLayerBlock:
     production_admitted = False
 
-    def __init__(self, block, ffn_fp8=False):
+    def __init__(self, block, ffn_fp8=False, ffn_act_fp8=False):
         """ffn_fp8=True runs FFN1/FFN2 with e4m3 weights and per-output-channel
-        fp32 scales (quantized once here); everything else stays bf16."""
+        fp32 scales (quantized once here); everything else stays bf16.
+        ffn_act_fp8=True (with ffn_fp8) also quantizes FFN1's input per row
+        (absmax / 448, inside LayerNorm 3) and runs FFN1 on the fp8 MFMA."""
         self.block = block
         self.ffn_fp8 = bool(ffn_fp8)
+        self.ffn_act_fp8 = bool(ffn_act_fp8)
         self.weights = block_parameters(block)
         self.eps = block_eps(block)
         self.context_rows = self.context_roots = None
@@ -33,7 +36,8 @@ class WholeLayerBlock:
 
     def bound(self):
         if self._bound is None:
-            self._bound = BoundWeights(self.weights, self.eps, self.block.attn1.heads, ffn_fp8=self.ffn_fp8)
+            self._bound = BoundWeights(self.weights, self.eps, self.block.attn1.heads, ffn_fp8=self.ffn_fp8,
+                                       ffn_act_fp8=self.ffn_act_fp8)
         return self._bound
 
     def prepare_context(self, context, precompute=False):
