@@ -81,6 +81,33 @@ def timed_steps(fn, steps, warmup, gate=None):
     return start.elapsed_time(end) / steps
 
 
+def graph_replay_ms(fn, steps, warmup, what):
+    """Capture one call of fn into a HIP graph (torch.cuda.graph) and time
+    `steps` replays; every replay's output must equal the eager output byte for
+    byte.  The reference quotes its block times as warm graph replays
+    (算子研究/wam_ops/optimized/prepared.py:1-4)."""
+    import torch
+    ref = fn().clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+
+    def replay():
+        g.replay()
+        return out
+    ms = timed_steps(replay, steps, warmup, gate=what)
+    if not torch.equal(out, ref):
+        raise OutputMismatch(f"{what}: the graph replay's output differs from the eager call's")
+    del g
+    return ms
+
+
 def cache_state(blocks, name="pos"):
     """Clones of every pool tensor (k, v, id, mask, is_pred) of the blocks."""
     return [{k: v.clone() for k, v in b.attn1.attn_caches[name].items()} for b in blocks]
@@ -412,6 +439,7 @@ def main():
             return layer(x, ctx, temb, freqs, timer=timer)
 
     ms = timed_steps(step, args.steps, args.warmup, gate="L4680")
+    gms = graph_replay_ms(step, args.steps, args.warmup, "L4680 graph replay")
     # Dominant kernel (FFN1 GEMM + GELU): HIP events around its launch on the
     # launch stream, over the same number of steps.
     ffn1 = stage_times(lib, step, args.steps, 1 << STAGE_FFN1)["ffn1"]
@@ -455,6 +483,9 @@ def main():
         "outputs_checked": "every timed loop's last output equals its first call's byte for byte; "
                            "read-only KV pools unchanged",
         "stages_us": {k: round(v * 1e3, 1) for k, v in stages.items()},
+        "graph_replay": {"us_per_layer": round(gms * 1e3, 1), "tokens_per_s": round(M / (gms * 1e-3), 1),
+                         "checked": "the layer captured once into a HIP graph; every timed replay's "
+                                    "output equals the eager call's byte for byte"},
     }
     # Per-unit lines of the same run (algorithmic FLOP as in the layer count):
     # C2 QKV + q/k RMSNorm + RoPE, C3 FFN (FFN1 + GELU + FFN2 + gated
