@@ -62,11 +62,14 @@ def test_linear_bias(dev, M, K, N, nseg):
 # issued ahead of the LDS staging as well as the stores.  (4680, 3072, 3072),
 # (4680, 14336, 3072) and (4500, 4160, 3072) run on 224-row tiles (21 row
 # tiles; the last one of 4500 holds 20 rows, over 65 k-tiles), every
-# epilogue included.
+# epilogue included.  (6240, 6144, 3072), (6240, 3072, 3072) and (6000,
+# 1024, 3072) run as one round of 320-row tiles (the last one of 6000 holds
+# 240 rows).
 @pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
                                    (4680, 256, 14336), (6240, 3072, 2816), (6240, 6144, 3072),
                                    (3900, 4160, 4352), (300, 512, 200), (4680, 3072, 3072),
-                                   (4680, 14336, 3072), (4500, 4160, 3072)])
+                                   (4680, 14336, 3072), (4500, 4160, 3072), (6240, 3072, 3072),
+                                   (6000, 1024, 3072)])
 def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     D = N
@@ -170,11 +173,13 @@ def test_rms_rope(dev, B, M, H):
 # 5120 rows, one segment: 256-row tiles in one round.  "per-sample": a
 # [2, tokens, 1, 64] table whose two samples differ (row m reads table row m,
 # no modulo), on the fused four-wave path (4680 rows) and on the norm pass
-# (520 rows).
+# (520 rows).  6240 rows, one segment: one round of 320-row tiles and the
+# norm pass.
 @pytest.mark.parametrize("M,nseg,grid", [(4680, 3, (6, 26, 30)), (4680, 1, None), (520, 3, (2, 10, 26)),
                                          (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30)),
                                          (4680, 3, (1, 12, 15)), (5120, 1, (5, 32, 32)),
-                                         (4680, 1, "per-sample"), (520, 1, "per-sample")])
+                                         (4680, 1, "per-sample"), (520, 1, "per-sample"),
+                                         (6240, 1, (2, 26, 30))])
 def test_linear_qk_norm(dev, M, nseg, grid):
     from wam_ops import ops, synthetic
     K = N = 3072

@@ -61,6 +61,7 @@ struct GemmCfg {
   // the later parts have most of a k-step to land before the next barrier.
   static constexpr int SPLIT = SPLIT_;
   static constexpr int BLOCKS = BLOCKS_;  // resident workgroups per CU
+  static constexpr int EPI_ROWS = 1 << 30;  // cap on the epilogue's fp32 rows per stage buffer
   static constexpr int SCHED = SCHED_;    // 2: all DS reads of the next k-step, then this
                                           // step's MFMAs; 0: the compiler's order
   static constexpr int kWaves = WGM * WGN;
@@ -301,7 +302,8 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
 
   // The epilogue's per-column operands are loaded before the k loop, so that
   // their latency is not at the end of the tile.
-  constexpr int RPO = (C::STAGE / (C::BN * 4)) / 32 * 32;  // fp32 rows per buffer
+  constexpr int RPO_FIT = (C::STAGE / (C::BN * 4)) / 32 * 32;
+  constexpr int RPO = RPO_FIT < C::EPI_ROWS ? RPO_FIT : C::EPI_ROWS;  // fp32 rows per buffer
   static_assert(RPO >= 32, "a stage buffer must hold 32 fp32 rows of the tile");
   constexpr int ROUND = RPO * C::STAGES;                 // rows staged per round
   constexpr int NROUNDS = (C::BM + ROUND - 1) / ROUND;
@@ -1120,6 +1122,15 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
 // MFMAs, loads issued in two parts.  The smaller tiles serve grids that would
 // not cover the chip with 256x256 tiles and the 128x128 tails.
 using Cfg256x256w8t2 = GemmCfg<256, 256, 64, 2, 4, 2, 1, 2, 2, 2>;
+// 320x256 tiles, eight waves of 160x64 (two stages of 72 KB, loads issued in
+// three parts): 6240 rows are 20 such tiles, so a 3072-column GEMM is one
+// round of 240 tiles on 256 CUs.  The epilogue stages 32 rows per buffer
+// (five rounds of 64 rows): a round's residual rows then take 32 registers
+// per lane next to the 160 accumulators (with 64 rows per buffer they took
+// 64, and the gated-residual kernel spilled to scratch).
+struct Cfg320x256w8 : GemmCfg<320, 256, 64, 2, 4, 2, 1, 2, 2, 3> {
+  static constexpr int EPI_ROWS = 32;
+};
 using Cfg256x128w4 = GemmCfg<256, 128, 64, 2, 2, 3>;
 using Cfg128x128w4 = GemmCfg<128, 128, 64, 2, 2, 3>;
 // fp8 e4m3 weights on the small tiles (64-byte LDS weight rows widened at
@@ -1381,6 +1392,19 @@ static bool w4_t224_wins(int M, int seg_n, int n_seg, int K, int cus, int64_t ws
   return c224 < c256 - 1e-9;
 }
 
+// One round of 320-row tiles, when that round is shorter than the 256-row
+// plan (a round plus a tail) and the 224-row plan has lost already: 6240 x
+// 3072 (240 tiles against 300 + a tail), measured alternating on one box:
+// bias 114 -> 102 us, plain residual 129 -> 115, gated residual 141 -> 121,
+// bias + q-norm pass 132 -> 118, and 6240 x 3072 x 14336 474 -> 463 us.
+static bool t320_one_round(int M, int seg_n, int n_seg, int K, int cus, int64_t ws_bytes) {
+  const int64_t nt = (int64_t)(seg_n / 256) * n_seg;
+  const int64_t t320 = (int64_t)((M + 319) / 320) * nt, t256 = (int64_t)((M + 255) / 256) * nt;
+  if (seg_n % 256 != 0 || t320 > cus) return false;
+  if (gemm_plan(M, seg_n, n_seg, K, cus, ws_bytes).kind == 0) return false;
+  return 320.0 / 256.0 < (double)(t256 / cus) + 0.4 - 1e-9;
+}
+
 // Whether linear() takes the 256x256 path for this shape.
 static bool uses_big_tiles(int M, int seg_n, int n_seg) {
   const int64_t big_tiles = (int64_t)((M + 255) / 256) * (seg_n / 256) * n_seg;
@@ -1531,6 +1555,10 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     if (w4_t224_wins(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes)) {
       if (norm) p.epi = kEpiBiasNorm;
       return launch_gemm<CfgW4t224>(p, s);
+    }
+    if (t320_one_round(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes)) {
+      WAM_TRY(launch_gemm<Cfg320x256w8>(p, s));
+      return norm ? linear_norm_pass(p, s) : WAM_OK;
     }
     if (res && a->K <= 4096) return launch_big<Cfg256x256w8t2, Cfg128x128w4>(p, ws_bytes, s);
     if (norm && gemm_plan(p.M, p.seg_n, p.n_seg_count, p.K, device_cu_count(), p.part ? ws_bytes : 0).kind == 0) {
