@@ -506,9 +506,13 @@ def main():
     variants = {
         "fp8_ffn_variant": (dict(ffn_fp8=True),
                             "e4m3 per-output-channel scales (absmax/448), bf16 activations, fp32 accumulate"),
-        "fp8_act_ffn_variant": (dict(ffn_fp8=True, ffn_act_fp8=True),
+        "fp8_act_ffn_variant": (dict(ffn_fp8=True, ffn_act_fp8=1),
                                 "e4m3 weights as above; FFN1 input e4m3 with per-row scales (absmax/448, "
                                 "written by LayerNorm 3) on the fp8 MFMA; FFN2 bf16 activations"),
+        "fp8_mx_ffn_variant": (dict(ffn_fp8=True, ffn_act_fp8=2),
+                               "e4m3 weights as above; FFN1 input e4m3 with per-row scales on the fp8 MFMA; "
+                               "hidden layer e4m3 with one e8m0 exponent per 32 values (MX), FFN2 on the fp8 "
+                               "MFMA with those block scales"),
     }
     for key, (opts, what) in variants.items():
         flayer = WholeLayerBlock(blk, **opts)

@@ -73,8 +73,10 @@ enum {
 };
 
 /* Element types; zero (a memset struct) means bf16. */
-enum { WAM_BF16 = 0, WAM_F32 = 1, WAM_FP8 = 2 /* OCP e4m3 (e4m3fn), weights only */,
-       WAM_I64 = 3, WAM_F64 = 4 /* grid ids of wam_rope_freqs only */ };
+enum { WAM_BF16 = 0, WAM_F32 = 1, WAM_FP8 = 2 /* OCP e4m3 (e4m3fn) */,
+       WAM_I64 = 3, WAM_F64 = 4 /* grid ids of wam_rope_freqs only */,
+       WAM_FP8_MX = 5 /* e4m3 values with one e8m0 exponent per 32 consecutive
+                        values of a row (an OCP MX block): value = q * 2^(e - 127) */ };
 
 /* Epilogues of wam_linear. */
 enum {
@@ -119,7 +121,8 @@ typedef struct {
   const void* res;   /* residual [M, seg_n], row stride ldr */
   int64_t ldr;
   int res_dtype;     /* WAM_BF16 | WAM_F32 */
-  int out_dtype;     /* WAM_BF16 | WAM_F32 (f32 only for the residual epilogues) */
+  int out_dtype;     /* WAM_BF16 | WAM_F32 (f32 only for the residual epilogues) |
+                        WAM_FP8_MX (below) */
   wam_modulation gate; /* gate row = mod[b, t, gate_index] for row m = b*tokens+t */
   int gate_index;
   /* Weight storage.  WAM_BF16, or WAM_FP8: e4m3 weights with one fp32 scale
@@ -159,8 +162,21 @@ typedef struct {
    * y = sum_k fp8(a[m,k]) fp8(w[n,k]) * a_scale[m] * w_scale[n] + b[n].
    * Needs fp8 weights, WAM_EPI_BIAS or WAM_EPI_BIAS_GELU, one segment of
    * whole 256-column tiles and K a multiple of 128.  Not in the reference
-   * (an fp8-activation variant of the FFN). */
+   * (an fp8-activation variant of the FFN).
+   * WAM_FP8_MX: a is e4m3 [M, K] with e8m0 exponents a_block_scale [M, K / 32]
+   * (bytes, row stride K / 32): y = sum_k q[m,k] 2^(e[m,k/32]-127) fp8(w[n,k])
+   * * w_scale[n] + b[n], the exponents applied by the MFMA itself.  Needs fp8
+   * weights, WAM_EPI_BIAS, WAM_EPI_BIAS_GATE_RES or WAM_EPI_BIAS_RES with a
+   * bf16 output, one segment of whole 256-column tiles and K a multiple of
+   * 128. */
   int a_dtype; const float* a_scale;
+  const void* a_block_scale;
+  /* out_dtype WAM_FP8_MX (a_dtype WAM_FP8, WAM_EPI_BIAS or WAM_EPI_BIAS_GELU):
+   * out[0] is e4m3 [M, seg_n] (ldo in bytes) and out_block_scale [M, seg_n /
+   * 32] the e8m0 exponent of each row's 32-column blocks, the smallest with
+   * max |y| <= 448 * 2^(e - 127) over the block; q = e4m3(y * 2^(127 - e)),
+   * round to nearest even.  The FFN1 -> FFN2 hand-over of the fp8 FFN. */
+  void* out_block_scale;
 } wam_linear_args;
 
 int wam_linear(const wam_linear_args* args, void* stream);
@@ -321,9 +337,13 @@ typedef struct {
   const float* ffn_scale[2];
   /* With ffn_fp8 set: ffn_act_fp8 = 1 also quantizes FFN1's input per row
    * (LayerNorm 3 writes e4m3 rows with absmax/448 scales, as wam_ln_args.y8)
-   * and runs FFN1 on the fp8 MFMA (wam_linear a_dtype = WAM_FP8).  Needs
+   * and runs FFN1 on the fp8 MFMA (wam_linear a_dtype = WAM_FP8).
+   * ffn_act_fp8 = 2 in addition has FFN1 write the GELU output as MX e4m3
+   * (out_dtype WAM_FP8_MX: one e8m0 exponent per row and 32 columns) and runs
+   * FFN2 on it (a_dtype WAM_FP8_MX): both FFN GEMMs on the fp8 MFMA.  Needs
    * ffn_dim to be a multiple of 256.  Workspace: the layout always holds the
-   * e4m3 rows and their scales. */
+   * e4m3 rows and their scales; the MX hidden layer fits in the bf16 one's
+   * bytes. */
   int ffn_act_fp8;
 } wam_block_weights;
 

@@ -53,3 +53,32 @@ def ffn_gated(x, w1, b1, w2, b2, residual, gate):
     oracle's FFN unit; model.py:790-793 with the bf16 roundings removed)."""
     h = F.gelu(x.float() @ w1.float().t() + b1.float(), approximate="tanh")
     return residual.float() + (h @ w2.float().t() + b2.float()) * gate.float()
+
+
+def mx_exponent(amax):
+    """e8m0 exponent X of an MX block (OCP MX: 32 e4m3 values sharing one
+    power-of-two scale 2^X) whose largest magnitude is amax: the smallest X
+    with amax <= 448 * 2^X, floored at -127.  amax float32 tensor, >= 0."""
+    m, e = torch.frexp(amax.double())        # amax = m * 2^e, m in [0.5, 1)
+    x = (e - 1 - 8).to(torch.int32)          # amax = (2m) 2^(e-1); 448 = 1.75 * 2^8
+    x = torch.where(2 * m > 1.75, x + 1, x)  # 2m > 1.75: the next power
+    x = torch.where(amax > 0, x, torch.full_like(x, -127))
+    return x.clamp(min=-127)
+
+
+def quantize_mx32(y):
+    """y [M, N] (N a multiple of 32) -> (q float8_e4m3fn [M, N], e uint8
+    [M, N / 32]) with e = X + 127 per 32-column block and q = e4m3(y * 2^-X),
+    round to nearest even (the scaled values stay within +-448)."""
+    yf = y.float()
+    M, N = yf.shape
+    blk = yf.reshape(M, N // 32, 32)
+    X = mx_exponent(blk.abs().amax(dim=2))
+    q = (blk * torch.pow(2.0, -X.double()).float()[..., None]).reshape(M, N).to(E4M3)
+    return q, (X + 127).to(torch.uint8)
+
+
+def dequantize_mx32(q, e):
+    M, N = q.shape
+    X = e.to(torch.int32) - 127
+    return (q.float().reshape(M, N // 32, 32) * torch.pow(2.0, X.double()).float()[..., None]).reshape(M, N)

@@ -215,13 +215,19 @@ def test_ln_modulate_fp8_rows(dev, D, xdtype):
     assert torch.equal(sc.cpu(), so) and torch.equal(q.cpu().view(torch.uint8).reshape(B * M, D), qo.view(torch.uint8))
 
 
-def test_block_with_fp8_ffn_activations(dev):
+@pytest.mark.parametrize("mode", [1, 2])
+def test_block_with_fp8_ffn_activations(dev, mode):
     """The block with e4m3 FFN weights and e4m3 FFN1 activations (quantized
-    per row inside LayerNorm 3).  FFN1 before GELU against the fp32 product of
-    the oracle's quantization of the block's own LayerNorm-3 rows and the
-    dequantized weight: the bf16 ulp bound (only the accumulation order and
-    the output rounding differ).  The output against the bf16-weight oracle
-    at the fp8 bound; a debug call leaves the output unchanged."""
+    per row inside LayerNorm 3); mode 2 also hands the hidden layer to FFN2
+    as MX e4m3 (both FFN GEMMs on the fp8 MFMA).  FFN1 before GELU against
+    the fp32 product of the oracle's quantization of the block's own
+    LayerNorm-3 rows and the dequantized weight: the bf16 ulp bound (only the
+    accumulation order and the output rounding differ).  Mode 2: the hidden
+    layer (dequantized debug copy) within half an e4m3 step of GELU of that
+    product plus the bf16 bound, and FFN2 before the gate against the fp32
+    product of that hidden layer and the dequantized weight at the bf16 ulp
+    bound.  The output against the bf16-weight oracle at the fp8 bound; a
+    debug call leaves the output unchanged."""
     from oracle.block import block_forward
     from wam_ops import synthetic
     from wam_ops.block import TransformerBlock
@@ -233,20 +239,125 @@ def test_block_with_fp8_ffn_activations(dev):
     with torch.no_grad():
         for name, prm in blk.named_parameters():
             prm.data = params[name].to(dev)
-    wl = WholeLayerBlock(blk.to(dev), ffn_fp8=True, ffn_act_fp8=True)
+    wl = WholeLayerBlock(blk.to(dev), ffn_fp8=True, ffn_act_fp8=mode)
     with torch.no_grad():
         wl.prepare_context(ctx.to(dev), precompute=True)
         out = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev))
         dbg = wl(x.to(dev), ctx.to(dev), temb.to(dev), freqs.to(dev), debug=True)
     torch.cuda.synchronize()
     assert torch.equal(dbg["output"], out), "a debug call changed the block output"
-    q1, s1, _, _ = wl.bound().ffn_fp8
+    q1, s1, q2, s2 = wl.bound().ffn_fp8
     h = dbg["modulated3"].reshape(-1, shape.dim).cpu()
     qh, sh = ofp8.quantize_rows(h)
     ffn1 = ofp8.dequantize_rows(qh, sh) @ ofp8.dequantize_rows(q1.cpu(), s1.cpu()).t() \
         + params["ffn.net.0.proj.bias"].float()
     got = dbg["ffn1"].reshape(ffn1.shape).cpu()
-    assert_close(got, ffn1, _ulp_bound(ffn1), 0.99999, "block fp8 FFN1 (fp8 activations)")
+    assert_close(got, ffn1, _ulp_bound(ffn1), 0.99999, f"block fp8 FFN1 (fp8 activations, mode {mode})")
+    if mode == 2:
+        g = torch.nn.functional.gelu(ffn1, approximate="tanh")
+        hid = dbg["gelu"].reshape(g.shape).cpu().float()
+        assert ((hid - g).abs() <= g.abs() * 2 ** -4 + _ulp_bound(g)).all()
+        ffn2 = hid @ ofp8.dequantize_rows(q2.cpu(), s2.cpu()).t() + params["ffn.net.2.bias"].float()
+        got2 = dbg["ffn2"].reshape(ffn2.shape).cpu()
+        assert_close(got2, ffn2, _ulp_bound(ffn2), 0.99999, "block MX FFN2 (before the gate)")
     ref = block_forward(params, x, ctx, temb, freqs, shape.heads, shape.eps)
-    m = assert_close(out.cpu(), ref, 0.5, 0.9995, "block fp8 FFN activations vs bf16-weight oracle")
-    print("block fp8 FFN activations", m)
+    m = assert_close(out.cpu(), ref, 0.5, 0.9995, f"block fp8 FFN activations mode {mode} vs bf16-weight oracle")
+    print(f"block fp8 FFN activations mode {mode}", m)
+
+
+# MX output of the fp8 MFMA (the FFN1 -> FFN2 hand-over of the fp8 FFN): e4m3
+# with one e8m0 exponent per row and 32 columns.  The same launch with a bf16
+# output rounds the same fp32 values y (same tiles, accumulation order and
+# epilogue math), so against that bf16 output yb: every value is within half
+# an e4m3 step at its block's exponent X (max(|yb| 2^-4, 2^(X-10))) plus the
+# bf16 rounding of yb (2^-8 |yb|); the exponents equal the oracle's rule on
+# the block maxima of yb except where the bf16 rounding of a maximum can
+# cross the rule's boundary (then by one).  Every nonzero block's largest
+# |q| lies in [224, 448]: the exponent is the smallest that keeps the block
+# within e4m3 (one too large would leave it below 224, one too small above
+# 448).  Against the fp32 product of the dequantized
+# operands, the dequantized output is within the e4m3 step plus the bf16
+# GEMM bound (2^-8 of the largest |y| + 2e-3).
+@pytest.mark.parametrize("M,K,N,gelu", [(4680, 3072, 14336, True), (300, 256, 512, False), (1, 3072, 256, True)])
+def test_fp8_mx_output(dev, M, K, N, gelu):
+    from wam_ops import ops
+    print(f"fp8 MX output {M}x{K}x{N} gelu={gelu}", flush=True)
+    x = _randn((M, K), dev, 31)
+    w = _randn((N, K), dev, 32, 0.02)
+    b = _randn((N,), dev, 33, 0.02)
+    qw, sw = ops.quantize_fp8_rows(w)
+    qx, sx = ops.quantize_fp8_rows(x)
+    epi = ops.EPI_BIAS_GELU if gelu else ops.EPI_BIAS
+    q, e = ops.linear(qx, qw, b, w_scale=sw, x_scale=sx, epilogue=epi, mx_out=True)
+    yb = ops.linear(qx, qw, b, w_scale=sw, x_scale=sx, epilogue=epi)
+    torch.cuda.synchronize()
+    assert q.dtype == torch.float8_e4m3fn and q.shape == (M, N) and e.shape == (M, N // 32)
+    q, e, yb = q.cpu(), e.cpu(), yb.float().cpu()
+    d = ofp8.dequantize_mx32(q, e)
+    half = torch.maximum(yb.abs() * 2 ** -4, torch.pow(2.0, e.double() - 127 - 10).float().repeat_interleave(32, 1))
+    assert ((d - yb).abs() <= half + yb.abs() * 2 ** -8 + 1e-30).all()
+    amax = yb.reshape(M, N // 32, 32).abs().amax(dim=2).double()
+    er = ofp8.mx_exponent(amax.float()) + 127
+    diff = e.int() != er
+    assert ((e.int() - er).abs() <= 1).all()
+    # a differing exponent only where the bf16 rounding of the block maximum
+    # can cross the rule's boundary 448 * 2^X (or 448 * 2^(X-1))
+    X = (er - 127).double()
+    near = torch.minimum((amax - 448 * torch.pow(2.0, X)).abs(), (amax - 448 * torch.pow(2.0, X - 1)).abs())
+    assert (near[diff] <= amax[diff] * 2 ** -8).all()
+    assert diff.float().mean().item() <= 0.01
+    bm = q.float().reshape(M, N // 32, 32).abs().amax(dim=2)
+    assert ((bm >= 224) | (bm == 0)).all() and (bm <= 448).all()
+    xd = ofp8.dequantize_rows(qx.cpu(), sx.cpu())
+    wd = ofp8.dequantize_rows(qw.cpu(), sw.cpu())
+    y = xd @ wd.t() + b.float().cpu()
+    if gelu:
+        y = torch.nn.functional.gelu(y, approximate="tanh")
+    assert ((d - y).abs() <= y.abs() * 2 ** -4 + _ulp_bound(y)).all()
+
+
+# MX activations into the fp8 MFMA (the FFN2 side): the operand is the
+# oracle's MX quantization of bf16 values; against the fp32 product of the
+# same dequantized operands the only differences are the accumulation order
+# and the output rounding (the bf16 ulp bound), for the bias, gated-residual
+# (fp32 residual stream, per-sample gate) and plain bf16 residual epilogues.
+@pytest.mark.parametrize("M,K,N", [(4680, 14336, 3072), (300, 256, 512), (1, 128, 256), (455, 1024, 256)])
+def test_fp8_mx_input(dev, M, K, N):
+    from wam_ops import ops
+    print(f"fp8 MX input {M}x{K}x{N}", flush=True)
+    x = _randn((M, K), dev, 41).float().cpu()
+    x[0, :32] = 0  # an all-zero block
+    qx, ex = ofp8.quantize_mx32(x)
+    w = _randn((N, K), dev, 42, 0.02)
+    b = _randn((N,), dev, 43, 0.02)
+    qw, sw = ops.quantize_fp8_rows(w)
+    ref = ofp8.dequantize_mx32(qx, ex).to(dev) @ ofp8.dequantize_rows(qw.cpu(), sw.cpu()).to(dev).t() + b.float()
+    qx, ex = qx.to(dev), ex.to(dev)
+    y = ops.linear(qx, qw, b, w_scale=sw, x_block_scale=ex)
+    assert_close(y, ref, _ulp_bound(ref), 0.99999, f"MX input bias {M}x{K}x{N}")
+    res32 = _randn((M, N), dev, 44, 1.0, torch.float32)
+    tokens = M // 2 if M % 2 == 0 else M
+    table = _randn((1, 6, N), dev, 45, 0.1, torch.float32)
+    temb = _randn((M // tokens, 1, 6, N), dev, 46, 0.1, torch.float32)
+    gate = (table[0, 5][None] + temb[:, 0, 5]).repeat_interleave(tokens, 0)
+    y = ops.linear(qx, qw, b, w_scale=sw, x_block_scale=ex, epilogue=ops.EPI_BIAS_GATE_RES, residual=res32,
+                   table=table, temb=temb, tokens=tokens, gate_index=5)
+    r = res32 + ref * gate
+    assert_close(y, r, _ulp_bound(r), 0.99999, f"MX input gated residual {M}x{K}x{N}")
+    res = _randn((M, N), dev, 47)
+    y = ops.linear(qx, qw, b, w_scale=sw, x_block_scale=ex, epilogue=ops.EPI_BIAS_RES, residual=res)
+    r = res.float() + ref
+    assert_close(y, r, _ulp_bound(r), 0.99999, f"MX input residual {M}x{K}x{N}")
+
+
+def test_fp8_mx_rejects(dev):
+    from wam_ops import ops
+    x = _randn((64, 256), dev, 1)
+    w = _randn((256, 256), dev, 2, 0.02)
+    qw, sw = ops.quantize_fp8_rows(w)
+    qx, ex = ofp8.quantize_mx32(x.float().cpu())
+    qx, ex = qx.to(dev), ex.to(dev)
+    with pytest.raises(RuntimeError, match="MX activations"):
+        ops.linear(qx, qw, None, w_scale=sw, x_block_scale=ex, epilogue=ops.EPI_BIAS_GELU)
+    with pytest.raises(RuntimeError, match="mx_out"):
+        ops.linear(x, w, None, mx_out=True)

@@ -12,8 +12,9 @@ computes, it does not return a cached result).
 
 * WholeLayerBlock at dim 3072 / 24 heads / FFN 14336 with 256 tokens over a
   1024-slot read-only pool (candidate rows, validated before the capture) and
-  512 precomputed context rows; also in the e4m3 FFN variant with e4m3 FFN1
-  activations.
+  512 precomputed context rows; also in the fp8 FFN variant with e4m3
+  weights and activations (FFN1 and FFN2 on the fp8 MFMA, the hidden layer
+  as MX e4m3).
 * BlockStack of three small layers with candidate rows (the one host
   read-back per forward happens before the capture, so the captured forward
   reads nothing back).
@@ -75,7 +76,7 @@ def test_whole_layer_graph_replay(dev, variant):
                                                  device=dev)
     x2, *_ = synthetic.block_inputs(shape, 2, M, (4, 8, 8), context_len=512, seed=64, device=dev)
     rows = torch.zeros(2, dtype=torch.int64, device=dev)
-    opts = dict(ffn_fp8=True, ffn_act_fp8=True) if variant == "fp8_act" else {}
+    opts = dict(ffn_fp8=True, ffn_act_fp8=2) if variant == "fp8_act" else {}
     wl = WholeLayerBlock(blk, **opts)
     junk = torch.randn(1 << 20, device=dev)
     with torch.no_grad():

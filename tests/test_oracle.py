@@ -191,3 +191,31 @@ def test_fp8_quantization_pinned():
     # relative error of a normal e4m3 value is at most 2^-4 (3 mantissa bits, RNE)
     nz = w.abs() > 0
     assert ((deq - w).abs()[nz] <= w.abs()[nz] * 2 ** -4 + 1e-12).all()
+
+
+def test_mx32_quantization_pinned():
+    """The oracle's MX (32-value block, e8m0 exponent) quantization: the
+    exponent's closed form at the boundaries (448 * 2^X is the largest block
+    max that keeps X), brute force over a range of exponents that it is the
+    smallest one with no value above 448, and the round trip."""
+    from oracle import fp8
+    cases = {448.0: 0, 448.0 * 1.0001: 1, 256.0: 0, 255.99: 0, 224.0: -1, 223.9: -1, 112.01: -1, 1.0: -8, 1.75: -8,
+             1.7501: -7, 3.5: -7, 0.0: -127, 2.0 ** -140: -127, 448.0 * 2 ** 20: 20}
+    for v, x in cases.items():
+        assert fp8.mx_exponent(torch.tensor([v], dtype=torch.float32)).item() == x, v
+    g = torch.Generator().manual_seed(5)
+    amax = torch.rand(4000, generator=g) * torch.pow(2.0, torch.randint(-30, 30, (4000,), generator=g).float())
+    X = fp8.mx_exponent(amax).double()
+    assert (amax.double() <= 448 * torch.pow(2.0, X)).all()
+    assert (amax.double() > 448 * torch.pow(2.0, X - 1)).all()
+    y = torch.randn(6, 128, generator=g) * torch.pow(2.0, torch.randint(-8, 8, (6, 1), generator=g).float())
+    y[1, 32:64] = 0
+    q, e = fp8.quantize_mx32(y)
+    assert e.shape == (6, 4) and e[1, 1].item() == 0 and not q.float()[1, 32:64].any()
+    blockmax = q.float().reshape(6, 4, 32).abs().amax(dim=2)
+    nz = blockmax > 0
+    assert (blockmax[nz] >= 224).all() and (blockmax <= 448).all()
+    d = fp8.dequantize_mx32(q, e)
+    # e4m3 keeps 3 mantissa bits: 2^-4 relative, or half the subnormal step 2^-10 at the block's scale
+    step = torch.pow(2.0, (e.double() - 127 - 10)).float().repeat_interleave(32, dim=1)
+    assert ((d - y).abs() <= torch.maximum(y.abs() * 2 ** -4, step) + 1e-30).all()

@@ -29,6 +29,7 @@
 namespace wam {
 
 int linear(const wam_linear_args*, hipStream_t);
+int mx_dequant_bf16(const void* q, const void* e, void* y, int rows, int cols, hipStream_t s);
 int ln_modulate(const wam_ln_args*, hipStream_t);
 int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
@@ -167,6 +168,7 @@ static int check_weights(const wam_block_weights* w) {
   WAM_REQUIRE(w->norm2_dtype == WAM_F32 || w->norm2_dtype == WAM_BF16, "block: norm2 dtype");
   WAM_REQUIRE(!w->ffn_fp8[0] || (w->ffn_fp8[1] && w->ffn_scale[0] && w->ffn_scale[1]),
               "block: fp8 FFN needs both weights and both scale vectors");
+  WAM_REQUIRE(w->ffn_act_fp8 >= 0 && w->ffn_act_fp8 <= 2, "block: ffn_act_fp8 must be 0, 1 or 2");
   WAM_REQUIRE(!w->ffn_act_fp8 || (w->ffn_fp8[0] && w->ffn_dim % 256 == 0),
               "block: fp8 FFN activations need the fp8 FFN weights and ffn_dim %% 256 == 0 (ffn_dim=%d)",
               w->ffn_dim);
@@ -241,6 +243,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   float* x1 = reinterpret_cast<float*>(ws + L.x1);
   float* x2 = reinterpret_cast<float*>(ws + L.x2);
   bf16* act = reinterpret_cast<bf16*>(ws + L.act);
+  // The MX hidden layer (ffn_act_fp8 = 2): e4m3 [R, F] at act, its e8m0
+  // exponents [R, F / 32] right after (within the bf16 layer's bytes).
+  uint8_t* act_mx = reinterpret_cast<uint8_t*>(ws + L.act) + (size_t)R * F;
   int32_t* slots = reinterpret_cast<int32_t*>(ws + L.slots);
   int32_t* newslots = reinterpret_cast<int32_t*>(ws + L.newslots);
   int32_t* info = reinterpret_cast<int32_t*>(ws + L.info);
@@ -291,6 +296,10 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     }
     if (wf8 == 0 && W->ffn_act_fp8) {
       g.a = h8; g.a_dtype = WAM_FP8; g.a_scale = h8s;  // the fused FFN1's own input
+    }
+    if (wf8 == 1 && W->ffn_act_fp8 == 2) {
+      // FFN2's own MX input
+      g.a = act; g.lda = F; g.a_dtype = WAM_FP8_MX; g.a_block_scale = act_mx;
     }
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     return linear(&g, s);
@@ -514,10 +523,18 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     if (W->ffn_act_fp8) {
       g.a = h8; g.a_dtype = WAM_FP8; g.a_scale = h8s;
     }
+    if (W->ffn_act_fp8 == 2) {
+      // e4m3 hidden layer with e8m0 exponents per 32 columns, FFN2's MX input
+      g.out_dtype = WAM_FP8_MX; g.out_block_scale = act_mx;
+    }
     g.workspace = split_ws; g.workspace_bytes = split_bytes;
     WAM_TRY(linear(&g, s));
   }
-  WAM_TRY(copy_debug(a->debug, 13, act, (size_t)R * F * 2, s));
+  if (W->ffn_act_fp8 == 2) {
+    if (dbg(13)) WAM_TRY(mx_dequant_bf16(act, act_mx, dbg(13), R, F, s));
+  } else {
+    WAM_TRY(copy_debug(a->debug, 13, act, (size_t)R * F * 2, s));
+  }
   if (dbg(24)) WAM_TRY(plain_linear(act, F, D, 25, 1, dbg(24)));
   // 15. FFN2 + gated residual (c_gate 5).
   {
@@ -527,6 +544,9 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
     g.epilogue = WAM_EPI_BIAS_GATE_RES; g.res = x2; g.ldr = D; g.res_dtype = WAM_F32;
     if (W->ffn_fp8[0]) {
       g.w[0] = W->ffn_fp8[1]; g.w_dtype = WAM_FP8; g.w_scale[0] = W->ffn_scale[1];
+    }
+    if (W->ffn_act_fp8 == 2) {
+      g.a_dtype = WAM_FP8_MX; g.a_block_scale = act_mx;
     }
     g.gate = mod; g.gate_index = 5;
     g.out_dtype = a->out_dtype;

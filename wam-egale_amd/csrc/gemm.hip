@@ -44,6 +44,12 @@ struct LinearParams {
   // fp8 e4m3 activations (the fp8 MFMA mode): A is [M, K] bytes with one
   // fp32 scale per row
   const float* ascale;
+  // MX activations: A is e4m3 [M, K] with one e8m0 exponent per row and 32
+  // consecutive k (abscale, row stride K / 32 bytes); MX output: out[0] is
+  // e4m3 [M, seg_n] (row stride ldo bytes) with one e8m0 exponent per row and
+  // 32 consecutive columns (oscale, row stride seg_n / 32 bytes).
+  const uint8_t* abscale;
+  uint8_t* oscale;
 };
 
 constexpr int kEpiPartial = 100;   // kernel epilogue of a split-K range: raw fp32 sums
@@ -579,12 +585,17 @@ __device__ __forceinline__ void w4_sched() {
 // k-step is then 128 values = 128 bytes per row, so staging, LDS layout and
 // epilogue are those of bf16 byte for byte; only the fragment reads (32 bytes
 // per lane) and the MFMA differ.
-template <int EPI, int RF32, int OF32, int TM, int WB = 2, bool F8MM = false>
+template <int EPI, int RF32, int OF32, int TM, int WB = 2, bool F8MM = false, bool AMX = false>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   static_assert(TM == 256 || TM == 224, "tile rows");
   static_assert(WB == 2 || WB == 1, "weight bytes");
-  static_assert(!F8MM || (WB == 2 && TM == 224 && (EPI == WAM_EPI_BIAS || EPI == WAM_EPI_BIAS_GELU)),
-                "fp8 MFMA: 224-row tiles, bias or GELU epilogue");
+  constexpr bool MXO = OF32 == 2;  // e4m3 output with e8m0 exponents per 32 columns
+  static_assert(!F8MM || (WB == 2 && TM == 224), "fp8 MFMA: 224-row tiles");
+  static_assert(!F8MM || AMX || EPI == WAM_EPI_BIAS || EPI == WAM_EPI_BIAS_GELU,
+                "fp8 MFMA with per-row activation scales: bias or GELU epilogue");
+  static_assert(!AMX || (F8MM && !MXO && EPI != WAM_EPI_BIAS_GELU), "MX activations: fp8 MFMA, bf16 output");
+  static_assert(!MXO || (F8MM && !AMX && (EPI == WAM_EPI_BIAS || EPI == WAM_EPI_BIAS_GELU)),
+                "MX output: fp8 MFMA with per-row activation scales, bias or GELU");
   constexpr int AE = F8MM ? 1 : 2;        // bytes per A element
   constexpr int WE = F8MM ? 1 : WB;       // bytes per W element
   constexpr int MB = TM == 256 ? 4 : 7;   // 32-row m-blocks per wave
@@ -693,61 +704,107 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   if constexpr (F8MM) {
   // fp8 MFMA k loop.  One staging set (k-step t+1 written to the free stage
   // and reloaded with t+2 during step t: one step of lead) and two sub-steps
-  // of 64 values per 128-byte k-step; a lane's fragment is 32 bytes of its
-  // row at logical chunks 4 s + 2 half and 4 s + 2 half + 1.
+  // of 64 values per 128-byte k-step.  The MFMA's k = 64 are two blocks of
+  // 32: block b is bytes 16 b .. 16 b + 15 of both lane halves, and its
+  // block scale comes from lane half b (measured on the device).  A lane of
+  // half h therefore takes logical chunks 4 s + h (block 2 s of the k-step)
+  // and 4 s + 2 + h (block 2 s + 1), so that each MFMA block is one 32-value
+  // block of the row.
   typedef int i32x8 __attribute__((ext_vector_type(8)));
   i32x8 ga[2][MB], gb[2][NB];
   const int rowa = (wm * 32 * MB + l32) * 128, rowb = 32768 + (wn * 32 * NB + l32) * 128;
   auto frag8 = [&](const char* p8, int s) {
-    const int sw = (l32 >> 1) & 7, c = 4 * s + 2 * half;
+    const int sw = (l32 >> 1) & 7, c = 4 * s + half;
     const u32x4s lo = *reinterpret_cast<const u32x4s*>(p8 + ((c ^ sw) << 4));
-    const u32x4s hi = *reinterpret_cast<const u32x4s*>(p8 + (((c + 1) ^ sw) << 4));
+    const u32x4s hi = *reinterpret_cast<const u32x4s*>(p8 + (((c + 2) ^ sw) << 4));
     return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
-  auto rd8 = [&](const char* buf, int s, int f) {
+  // AMX: the e8m0 exponents of the A tile's rows for a k-step (4 bytes =
+  // 4 blocks of 32 per row) ride with the stage, thread t loading row t
+  // into bytes 28672 + 4 t (free: the A rows end at 28672, W starts at
+  // 32768).  Lane half h supplies the scale of MFMA block h, i.e. of the
+  // k-step's block 2 s + h: its rows' words shifted right by 8 h hold that
+  // of sub-step 0 in byte 0 and that of sub-step 1 in byte 2, which the
+  // MFMA's operand select picks.
+  constexpr int kScl = 28672;
+  const uint32_t ldsc = (uint32_t)p.K / 32u;  // exponent bytes per A row
+  const __amdgpu_buffer_rsrc_t rsc =
+      AMX ? make_rsrc(p.abscale + (int64_t)m0 * ldsc, (uint32_t)(p.M - m0) * ldsc) : make_rsrc(p.a, 0u);
+  uint32_t ssc = 0;
+  uint32_t scw[2][MB];
+  auto rd8 = [&](const char* buf, int s, int f, int par) {
 #pragma unroll
     for (int i = 0; i < MB; ++i) ga[f][i] = frag8(buf + rowa + i * 4096, s);
 #pragma unroll
     for (int j = 0; j < NB; ++j) gb[f][j] = frag8(buf + rowb + j * 4096, s);
+    if (AMX && s == 0) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        scw[par][i] = *reinterpret_cast<const uint32_t*>(buf + kScl + (wm * 32 * MB + 32 * i + l32) * 4) >> (8 * half);
+    }
   };
-  auto mm8 = [&](int f) {
+  auto mm8 = [&](int f, int par) {
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
-        acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(gb[f][j], ga[f][i], acc[j][i], 0, 0, 0, 127,
-                                                                    0, 127);
+      for (int i = 0; i < MB; ++i) {
+        if constexpr (AMX) {
+          if (f == 0)
+            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(gb[f][j], ga[f][i], acc[j][i], 0, 0, 0, 127,
+                                                                        0, (int)scw[par][i]);
+          else
+            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(gb[f][j], ga[f][i], acc[j][i], 0, 0, 0, 127,
+                                                                        2, (int)scw[par][i]);
+        } else {
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(gb[f][j], ga[f][i], acc[j][i], 0, 0, 0, 127,
+                                                                      0, 127);
+        }
+      }
+  };
+  auto gsc = [&](int kt) {
+    if constexpr (AMX) ssc = __builtin_amdgcn_raw_buffer_load_b32(rsc, tid * (int)ldsc + kt * 4, 0, 0);
+  };
+  auto wsc8 = [&](char* buf) {
+    if constexpr (AMX) *reinterpret_cast<uint32_t*>(buf + kScl + tid * 4) = ssc;
   };
   // Prologue: k-step 0 into L0, k-step 1 into the staging set.
   gload(S0, 0, I0{}, INL{});
+  gsc(0);
   swrite(S0, L0, I0{}, INL{});
+  wsc8(L0);
   gload(S0, min(1, nk - 1), I0{}, INL{});
+  gsc(min(1, nk - 1));
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
-  rd8(L0, 0, 0);
+  rd8(L0, 0, 0, 0);
   // Step t: sub-step 0 from `cur` with the writes of k-step t+1 to `nxt` and
   // the loads of k-step t+2; the barrier; sub-step 1 with the reads of the
-  // next step's sub-step 0 from `nxt`.
-  auto kstep8 = [&](int t, char* cur, char* nxt) {
-    rd8(cur, 1, 1);
+  // next step's sub-step 0 from `nxt`.  PAR = t % 2 picks the exponent words.
+  auto kstep8 = [&](int t, char* cur, char* nxt, auto par_c) {
+    constexpr int PAR = decltype(par_c)::value;
+    rd8(cur, 1, 1, PAR);
     swrite(S0, nxt, I0{}, INL{});
+    wsc8(nxt);
     gload(S0, min(t + 2, nk - 1), I0{}, INL{});
-    mm8(0);
-    w4_sched<NL, NL, NM, NR * 2>();
+    gsc(min(t + 2, nk - 1));
+    mm8(0, PAR);
+    w4_sched<NL + (AMX ? 1 : 0), NL + (AMX ? 1 : 0), NM, NR * 2>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
-    rd8(nxt, 0, 0);
-    mm8(1);
-    w4_sched<0, 0, NM, NR * 2>();
+    rd8(nxt, 0, 0, 1 - PAR);
+    mm8(1, PAR);
+    w4_sched<0, 0, NM, NR * 2 + (AMX ? MB : 0)>();
     __builtin_amdgcn_sched_barrier(0);
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   int t = 0;
   for (; t + 1 < nk; t += 2) {
-    kstep8(t, L0, L1);
-    kstep8(t + 1, L1, L0);
+    kstep8(t, L0, L1, P0{});
+    kstep8(t + 1, L1, L0, P1{});
   }
-  if (t < nk) kstep8(t, L0, L1);
+  if (t < nk) kstep8(t, L0, L1, P0{});
   } else {
   // Fragments of a sub-step: rows wm*32*MB + 32 i + l32 of A and wn*32*NB +
   // 32 j + l32 of W at logical chunk 2 s + half; the swizzle term is
@@ -857,7 +914,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
   constexpr bool PART = EPI == kEpiPartial;
   constexpr int RB = RF32 ? 4 : 2;                 // residual bytes per element
-  constexpr int OB = (OF32 || PART) ? 4 : 2;       // output bytes per element
+  constexpr int OB = PART ? 4 : (MXO ? 1 : (OF32 ? 4 : 2));  // output bytes per element
   // Rows of this tile that exist (the resources start at row m0, so their
   // bounds cover at most TM rows and stay far below 2^32 bytes).
   const uint32_t rows_left = (uint32_t)min(p.M - m0, TM);
@@ -881,6 +938,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     rout = make_rsrc(obase, (uint32_t)((rows_left - 1) * (uint32_t)ld + 256u) * OB);
   }
   const int ld_out = PART ? p.seg_n : (int)p.ldo;
+  // MX output exponents of this tile: rows m0.., the tile's 8 column blocks
+  const __amdgpu_buffer_rsrc_t rmxs =
+      MXO ? make_rsrc(p.oscale + (int64_t)m0 * (p.seg_n / 32) + n0 / 32,
+                      (uint32_t)((rows_left - 1) * (uint32_t)(p.seg_n / 32) + 8u))
+          : make_rsrc(p.a, 0u);
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
   typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
   // Tile row handled by pass ps (0..31) of round r: rows 64 r .. +64 of each
@@ -1011,7 +1073,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           continue;
         }
         float y[4];
-        if constexpr (F8MM) {
+        if constexpr (F8MM && AMX) {
+          // the MX exponents were applied by the MFMA; the column scale here
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = vv[k8][e] * wsc[e] + bv[e];
+        } else if constexpr (F8MM) {
           // row scale of the fp8 activations times the column scale
           const float sr = p.ascale[min(m0 + row, p.M - 1)];
 #pragma unroll
@@ -1051,7 +1117,19 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
             for (int e = 0; e < 4; ++e) y[e] = rv[e] + y[e];
           }
         }
-        if constexpr (OF32 && RES) {
+        if constexpr (MXO) {
+          // e4m3 with one e8m0 exponent per 32 columns (8 lanes): the block's
+          // largest |y| sets it, every value is scaled by an exact power of two
+          const float amax = max8_lanes(fmaxf(fmaxf(fabsf(y[0]), fabsf(y[1])), fmaxf(fabsf(y[2]), fabsf(y[3]))));
+          const int X = mx_exponent(amax);
+          const float inv = __uint_as_float((uint32_t)(127 - X) << 23);
+          int pk = 0;
+          pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[0] * inv, y[1] * inv, pk, false);
+          pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[2] * inv, y[3] * inv, pk, true);
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)pk, rout, off, 0, 0);
+          if ((q & 7) == 0)
+            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(X + 127), rmxs, row * (int)(p.seg_n / 32) + (q >> 3), 0, 0);
+        } else if constexpr (OF32 && RES) {
           __builtin_amdgcn_raw_buffer_store_b128(u32x4v{__float_as_uint(y[0]), __float_as_uint(y[1]),
                                                         __float_as_uint(y[2]), __float_as_uint(y[3])},
                                                  rout, off, 0, 0);
@@ -1435,11 +1513,14 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a->seg_n % 8 == 0 && (a->n_seg == 1 || a->seg_n % 128 == 0),
               "wam_linear: N=%d must be a multiple of 8 (of 128 with several segments)", a->seg_n);
   WAM_REQUIRE(a->w_dtype == WAM_BF16 || a->w_dtype == WAM_FP8, "wam_linear: w_dtype %d", a->w_dtype);
-  WAM_REQUIRE(a->a_dtype == WAM_BF16 || a->a_dtype == WAM_FP8, "wam_linear: a_dtype %d", a->a_dtype);
+  WAM_REQUIRE(a->a_dtype == WAM_BF16 || a->a_dtype == WAM_FP8 || a->a_dtype == WAM_FP8_MX,
+              "wam_linear: a_dtype %d", a->a_dtype);
   const bool f8 = a->w_dtype == WAM_FP8;
   const bool a8 = a->a_dtype == WAM_FP8;
+  const bool amx = a->a_dtype == WAM_FP8_MX;
+  const bool mxo = a->out_dtype == WAM_FP8_MX;
   const int wb = f8 ? 1 : 2;
-  WAM_REQUIRE((a->lda * (a8 ? 1 : 2)) % 16 == 0 && (a->ldw * wb) % 16 == 0 && a->ldo % 4 == 0,
+  WAM_REQUIRE((a->lda * (a8 || amx ? 1 : 2)) % 16 == 0 && (a->ldw * wb) % 16 == 0 && a->ldo % 4 == 0,
               "wam_linear: row strides must keep 16-byte alignment");
   WAM_REQUIRE(a->a != nullptr, "wam_linear: null activation");
   WAM_REQUIRE((int64_t)a->M * a->lda * 2 < (int64_t)1 << 31 && (int64_t)a->seg_n * a->ldw * wb < (int64_t)1 << 31,
@@ -1454,11 +1535,15 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   WAM_REQUIRE(a->epilogue >= WAM_EPI_BIAS && a->epilogue <= WAM_EPI_BIAS_RES,
               "wam_linear: unknown epilogue %d", a->epilogue);
   WAM_REQUIRE((a->res_dtype == WAM_BF16 || a->res_dtype == WAM_F32) &&
-              (a->out_dtype == WAM_BF16 || a->out_dtype == WAM_F32), "wam_linear: dtype codes");
+              (a->out_dtype == WAM_BF16 || a->out_dtype == WAM_F32 || mxo), "wam_linear: dtype codes");
   if (a->epilogue == WAM_EPI_BIAS_GATE_RES || a->epilogue == WAM_EPI_BIAS_RES)
     WAM_REQUIRE(a->res != nullptr && a->ldr % 4 == 0, "wam_linear: residual missing");
   else
-    WAM_REQUIRE(a->out_dtype == WAM_BF16, "wam_linear: fp32 output only for residual epilogues");
+    WAM_REQUIRE(a->out_dtype != WAM_F32, "wam_linear: fp32 output only for residual epilogues");
+  WAM_REQUIRE(!mxo || (a8 && (a->epilogue == WAM_EPI_BIAS || a->epilogue == WAM_EPI_BIAS_GELU) &&
+                       a->out_block_scale != nullptr),
+              "wam_linear: an MX output needs fp8 activations with row scales, WAM_EPI_BIAS or "
+              "WAM_EPI_BIAS_GELU, and out_block_scale");
   if (a->epilogue == WAM_EPI_BIAS_GATE_RES) {
     WAM_TRY(check_modulation(a->gate, a->M, "wam_linear"));
     WAM_REQUIRE(a->gate.temb_mods != 1 && a->gate_index >= 0 && a->gate_index < 6,
@@ -1509,25 +1594,52 @@ int linear(const wam_linear_args* a, hipStream_t s) {
     p.ssq_ld = (a->seg_n + 255) / 256;
   }
   const bool big = uses_big_tiles(a->M, a->seg_n, a->n_seg);
-  if (a8) {
-    WAM_REQUIRE(f8 && a->a_scale != nullptr, "wam_linear: fp8 activations need fp8 weights and a_scale");
-    WAM_REQUIRE((a->epilogue == WAM_EPI_BIAS || a->epilogue == WAM_EPI_BIAS_GELU) && !norm,
-                "wam_linear: fp8 activations take WAM_EPI_BIAS or WAM_EPI_BIAS_GELU");
+  if (a8 || amx) {
+    WAM_REQUIRE(f8 && (amx ? a->a_block_scale != nullptr : a->a_scale != nullptr),
+                "wam_linear: fp8 activations need fp8 weights and a_scale (a_block_scale for WAM_FP8_MX)");
+    if (a8)
+      WAM_REQUIRE((a->epilogue == WAM_EPI_BIAS || a->epilogue == WAM_EPI_BIAS_GELU) && !norm,
+                  "wam_linear: fp8 activations with row scales take WAM_EPI_BIAS or WAM_EPI_BIAS_GELU");
+    else
+      WAM_REQUIRE(a->epilogue != WAM_EPI_BIAS_GELU && !norm &&
+                  (a->out_dtype == WAM_BF16 || (a->out_dtype == WAM_F32 && a->epilogue == WAM_EPI_BIAS_GATE_RES &&
+                                                a->res_dtype == WAM_F32)),
+                  "wam_linear: MX activations take WAM_EPI_BIAS, WAM_EPI_BIAS_GATE_RES or WAM_EPI_BIAS_RES "
+                  "with a bf16 output (fp32 only for the gated fp32 residual)");
     WAM_REQUIRE(a->n_seg == 1 && a->seg_n % 256 == 0 && a->K % 128 == 0,
                 "wam_linear: fp8 activations need one segment, N a multiple of 256 and K of 128 (N=%d K=%d)",
                 a->seg_n, a->K);
     p.ascale = a->a_scale;
+    p.abscale = static_cast<const uint8_t*>(a->a_block_scale);
+    p.oscale = static_cast<uint8_t*>(a->out_block_scale);
     p.n_tiles_per_seg = a->seg_n / 256;
     p.m_tiles = (a->M + 223) / 224;
     p.n_tiles = p.n_tiles_per_seg;
     const dim3 grid((unsigned)(p.m_tiles * p.n_tiles));
-    if (a->epilogue == WAM_EPI_BIAS)
-      hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GELU, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
+    if (amx) {
+      if (a->epilogue == WAM_EPI_BIAS)
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS, 0, 0, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+      else if (a->epilogue == WAM_EPI_BIAS_GATE_RES && p.res_f32 && p.out_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GATE_RES, 1, 1, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+      else if (a->epilogue == WAM_EPI_BIAS_GATE_RES && p.res_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GATE_RES, 1, 0, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+      else if (a->epilogue == WAM_EPI_BIAS_GATE_RES)
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GATE_RES, 0, 0, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+      else if (p.res_f32)
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_RES, 1, 0, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_RES, 0, 0, 224, 2, true, true>), grid, dim3(256), 0, s, p);
+    } else if (a->epilogue == WAM_EPI_BIAS) {
+      if (mxo) hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS, 0, 2, 224, 2, true>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
+    } else {
+      if (mxo) hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GELU, 0, 2, 224, 2, true>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((gemm_w4_kernel<WAM_EPI_BIAS_GELU, 0, 0, 224, 2, true>), grid, dim3(256), 0, s, p);
+    }
     WAM_LAUNCHED("gemm_w4_kernel (fp8 MFMA)");
     return WAM_OK;
   }
+  WAM_REQUIRE(!mxo, "wam_linear: an MX output needs fp8 activations with row scales");
   if (f8) {
     // fp8 weights: the four-wave kernel widens them to bf16 as it stages
     // them (FFN unit at 4680 rows, alternating runs on one box: 713-714 us
@@ -1572,6 +1684,37 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   if (mid_tiles >= 200) WAM_TRY(launch_gemm<Cfg256x128w4>(p, s));
   else WAM_TRY(launch_gemm<Cfg128x128w4>(p, s));
   return norm ? linear_norm_pass(p, s) : WAM_OK;
+}
+
+// bf16 copy of an MX matrix (e4m3 q [rows, cols] with an e8m0 exponent per
+// row and 32 columns): a debug view of the fp8 FFN's hidden layer.  Every
+// e4m3 value times a power of two in bf16 range is a bf16 value (exact).
+__global__ __launch_bounds__(256) void mx_dequant_bf16_kernel(const uint8_t* __restrict__ q,
+                                                              const uint8_t* __restrict__ e, bf16* __restrict__ y,
+                                                              int cols, int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const int64_t idx = i * 4, r = idx / cols;
+  const int c = (int)(idx - r * cols);
+  const uint32_t v = *reinterpret_cast<const uint32_t*>(q + idx);
+  const float sc = __uint_as_float((uint32_t)e[r * (cols / 32) + c / 32] << 23);
+  bf16x4 o;
+  o[0] = static_cast<bf16>(__builtin_amdgcn_cvt_f32_fp8((int)v, 0) * sc);
+  o[1] = static_cast<bf16>(__builtin_amdgcn_cvt_f32_fp8((int)v, 1) * sc);
+  o[2] = static_cast<bf16>(__builtin_amdgcn_cvt_f32_fp8((int)v, 2) * sc);
+  o[3] = static_cast<bf16>(__builtin_amdgcn_cvt_f32_fp8((int)v, 3) * sc);
+  *reinterpret_cast<bf16x4*>(y + idx) = o;
+}
+
+int mx_dequant_bf16(const void* q, const void* e, void* y, int rows, int cols, hipStream_t s) {
+  WAM_REQUIRE(rows >= 0 && cols % 32 == 0, "mx_dequant_bf16: cols=%d must be a multiple of 32", cols);
+  const int64_t n4 = (int64_t)rows * cols / 4;
+  if (n4 == 0) return WAM_OK;
+  hipLaunchKernelGGL(mx_dequant_bf16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(q), static_cast<const uint8_t*>(e), static_cast<bf16*>(y), cols,
+                     n4);
+  WAM_LAUNCHED("mx_dequant_bf16_kernel");
+  return WAM_OK;
 }
 
 // Per-row fp8 e4m3 quantization: one workgroup per row.

@@ -288,6 +288,25 @@ __device__ inline float wave_max(float v) {
                      __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48))));
 }
 
+// Max over each aligned group of 8 lanes (quad exchanges, then the mirror
+// of the 8-lane half row); every lane of a group gets the group's max.
+__device__ inline float max8_lanes(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  return fmaxf(v, dpp<0x141>(v));
+}
+
+// e8m0 exponent of an MX block of e4m3 values (OCP MX: one power-of-two
+// scale per 32 values): the smallest X with amax <= 448 * 2^X, so that no
+// scaled value exceeds the e4m3 maximum.  With amax = m * 2^E, m in [1, 2):
+// X = E - 8 when m <= 1.75 (448 = 1.75 * 2^8), else E - 7.  Floored at -127
+// (amax 0 or subnormal); amax must be finite and >= 0.
+__device__ inline int mx_exponent(float amax) {
+  const uint32_t b = __float_as_uint(amax);
+  const int X = (int)(b >> 23) - 135 + ((b & 0x7fffffu) > 0x600000u ? 1 : 0);
+  return X < -127 ? -127 : X;
+}
+
 // Eight sums over the 64 lanes of a wave at once: v[k] summed over all lanes
 // lands in out[j] for k = j + 2 (r & 1) + 4 (r >> 1), r = lane / 16, on all
 // 16 lanes of row r.  Two halving exchanges (v_permlane32_swap trades the

@@ -14,7 +14,7 @@ LIB_NAME = "libwam_block.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 WAM_OK, WAM_ERR_ARG, WAM_ERR_HIP, WAM_ERR_STATE = 0, -1, -2, -3
-WAM_BF16, WAM_F32, WAM_FP8, WAM_I64, WAM_F64 = 0, 1, 2, 3, 4
+WAM_BF16, WAM_F32, WAM_FP8, WAM_I64, WAM_F64, WAM_FP8_MX = 0, 1, 2, 3, 4, 5
 WAM_ACT_NONE, WAM_ACT_SILU = 0, 1
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_GATE_RES, EPI_BIAS_RES = 0, 1, 2, 3
 PEAK_BF16_32, PEAK_BF16_16, PEAK_FP8_32, PEAK_FP8_16 = 0, 1, 2, 3
@@ -47,7 +47,8 @@ class LinearArgs(Structure):
                 ("workspace", c_void_p), ("workspace_bytes", c_int64),
                 ("norm_ssq", c_void_p * 3), ("norm_gamma", c_void_p * 3), ("norm_freq", c_void_p),
                 ("norm_freq_batch", c_int), ("norm_tokens", c_int), ("norm_head_dim", c_int),
-                ("a_dtype", c_int), ("a_scale", c_void_p)]
+                ("a_dtype", c_int), ("a_scale", c_void_p), ("a_block_scale", c_void_p),
+                ("out_block_scale", c_void_p)]
 
 
 class LnArgs(Structure):

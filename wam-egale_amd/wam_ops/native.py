@@ -78,9 +78,12 @@ class BoundWeights:
             st.ffn_fp8[0], st.ffn_fp8[1] = q1.data_ptr(), q2.data_ptr()
             st.ffn_scale[0], st.ffn_scale[1] = s1.data_ptr(), s2.data_ptr()
         if ffn_act_fp8:
-            # FFN1 input quantized per row inside LayerNorm 3, FFN1 on the fp8 MFMA
+            # 1: FFN1 input quantized per row inside LayerNorm 3, FFN1 on the
+            # fp8 MFMA; 2: also the hidden layer as MX e4m3 and FFN2 on the
+            # fp8 MFMA
             _check(ffn_fp8, "fp8 FFN activations need the fp8 FFN weights")
-            st.ffn_act_fp8 = 1
+            _check(int(ffn_act_fp8) in (1, 2), "ffn_act_fp8 must be 0, 1 (FFN1) or 2 (FFN1 and FFN2)")
+            st.ffn_act_fp8 = int(ffn_act_fp8)
         self.struct = st
 
 

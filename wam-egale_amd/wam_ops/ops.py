@@ -104,7 +104,8 @@ def quantize_fp8_rows(w, out=None, scale=None):
 
 def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=None,
            temb=None, tokens=None, gate_index=None, out=None, out_dtype=torch.bfloat16, w_scale=None,
-           norm_gamma=None, norm_freq=None, norm_head_dim=128, x_scale=None):
+           norm_gamma=None, norm_freq=None, norm_head_dim=128, x_scale=None, x_block_scale=None,
+           mx_out=False):
     """Y = epilogue(x W^T + b) on MFMA.  weights: one tensor or a list of up to 3
     (one launch, outputs split per weight).  Returns a tensor or a list.
     The residual may be bf16 or fp32; out_dtype=float32 is allowed for the
@@ -122,7 +123,13 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
     x may be float8_e4m3fn with x_scale, fp32 [M] per-row scales (from
     quantize_fp8_rows), when the weights are fp8 too: the product then runs
     on the fp8 MFMA, y = acc * x_scale[m] * w_scale[n] + b (bias or GELU
-    epilogue, one weight, N a multiple of 256, K of 128)."""
+    epilogue, one weight, N a multiple of 256, K of 128).  mx_out=True (fp8
+    x with x_scale) returns (q, e): q float8_e4m3fn [M, N] and e uint8 [M,
+    N / 32], one e8m0 exponent per row and 32 columns (y = q * 2^(e - 127)).
+    x may instead carry x_block_scale, uint8 [M, K / 32] e8m0 exponents of
+    its 32-value blocks (an MX operand, e.g. an mx_out result): the MFMA
+    applies them, y = acc * w_scale[n] + b with the bias, gated-residual or
+    residual epilogue and a bf16 output."""
     single = torch.is_tensor(weights)
     ws = [weights] if single else list(weights)
     bs = [biases] if (single or biases is None) else list(biases)
@@ -139,12 +146,17 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         _req(w_scale is None, "w_scale is only for fp8 weights")
     dev = _dev(x, *ws, *[b for b in bs if b is not None], residual, *scs, x_scale)
     x8 = x.dtype == FP8
-    if x8:
+    xmx = x8 and x_block_scale is not None
+    if xmx:
+        _req(f8 and x_scale is None and x_block_scale.dtype == torch.uint8 and x_block_scale.is_contiguous(),
+             "MX activations need fp8 weights and uint8 x_block_scale [M, K / 32] (no x_scale)")
+    elif x8:
         _req(f8 and x_scale is not None and x_scale.dtype == torch.float32 and x_scale.is_contiguous(),
              "fp8 activations need fp8 weights and fp32 x_scale [M]")
     else:
-        _req(x_scale is None, "x_scale is only for fp8 activations")
+        _req(x_scale is None and x_block_scale is None, "x_scale / x_block_scale are only for fp8 activations")
         _bf16(x, "x")
+    _req(not mx_out or (x8 and not xmx and single and out is None), "mx_out needs fp8 x with x_scale, one weight")
     _req(x.dim() >= 2 and x.stride(-1) == 1, "x must have a contiguous last dim")
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
@@ -161,6 +173,8 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         if b is not None:
             _bf16(b, "bias")
             _req(b.is_contiguous() and b.numel() == N, "bias must be [N]")
+    if mx_out:
+        out_dtype = FP8
     outs = out if out is not None else [torch.empty(*x.shape[:-1], N, dtype=out_dtype, device=dev)
                                         for _ in ws]
     if torch.is_tensor(outs):
@@ -179,8 +193,17 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
         a.w_dtype = _lib.WAM_FP8
         for i, sc in enumerate(scs):
             a.w_scale[i] = sc.data_ptr()
-    a.out_dtype = dtype_code(outs[0])
-    if x8:
+    mx_scale = None
+    if mx_out:
+        _req(N % 32 == 0, "mx_out needs N a multiple of 32")
+        mx_scale = torch.empty(M, N // 32, dtype=torch.uint8, device=dev)
+        a.out_dtype, a.out_block_scale = _lib.WAM_FP8_MX, mx_scale.data_ptr()
+    else:
+        a.out_dtype = dtype_code(outs[0])
+    if xmx:
+        _req(K % 32 == 0 and x_block_scale.shape == (M, K // 32), "x_block_scale must be [M, K / 32]")
+        a.a_dtype, a.a_block_scale = _lib.WAM_FP8_MX, x_block_scale.data_ptr()
+    elif x8:
         _req(x_scale.numel() == M, "x_scale must be [M]")
         a.a_dtype, a.a_scale = _lib.WAM_FP8, x_scale.data_ptr()
     ssqs = None
@@ -224,6 +247,8 @@ def linear(x, weights, biases=None, *, epilogue=EPI_BIAS, residual=None, table=N
     if scratch is not None:
         scratch.record_stream(torch.cuda.current_stream(dev))
     res = outs[0] if single else outs
+    if mx_out:
+        return res, mx_scale
     if ssqs is not None:
         return res, (ssqs[0] if single else ssqs)
     return res

@@ -22,11 +22,13 @@ class WholeLayerBlock:
     def __init__(self, block, ffn_fp8=False, ffn_act_fp8=False):
         """ffn_fp8=True runs FFN1/FFN2 with e4m3 weights and per-output-channel
         fp32 scales (quantized once here); everything else stays bf16.
-        ffn_act_fp8=True (with ffn_fp8) also quantizes FFN1's input per row
-        (absmax / 448, inside LayerNorm 3) and runs FFN1 on the fp8 MFMA."""
+        ffn_act_fp8=True / 1 (with ffn_fp8) also quantizes FFN1's input per row
+        (absmax / 448, inside LayerNorm 3) and runs FFN1 on the fp8 MFMA;
+        ffn_act_fp8=2 also hands the hidden layer to FFN2 as MX e4m3 (one
+        e8m0 exponent per 32 values) and runs FFN2 on the fp8 MFMA."""
         self.block = block
         self.ffn_fp8 = bool(ffn_fp8)
-        self.ffn_act_fp8 = bool(ffn_act_fp8)
+        self.ffn_act_fp8 = int(ffn_act_fp8)
         self.weights = block_parameters(block)
         self.eps = block_eps(block)
         self.context_rows = self.context_roots = None
