@@ -1055,6 +1055,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     for (int b8 = 0; b8 < nps / 8; ++b8) {
       f32x4 vv[8];
       float ssr[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int xkeep = 0;  // MXO: the exponent of pass (lane & 7) of this batch, for lane's block
 #pragma unroll
       for (int k8 = 0; k8 < 8; ++k8) {
         const int ps = b8 * 8 + k8;
@@ -1127,8 +1128,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[0] * inv, y[1] * inv, pk, false);
           pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[2] * inv, y[3] * inv, pk, true);
           __builtin_amdgcn_raw_buffer_store_b32((uint32_t)pk, rout, off, 0, 0);
-          if ((q & 7) == 0)
-            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(X + 127), rmxs, row * (int)(p.seg_n / 32) + (q >> 3), 0, 0);
+          // every lane of the 8-lane group holds X; lane k8 of it keeps it for
+          // one store of the batch's 8 rows x 8 blocks below
+          xkeep = (q & 7) == k8 ? X + 127 : xkeep;
         } else if constexpr (OF32 && RES) {
           __builtin_amdgcn_raw_buffer_store_b128(u32x4v{__float_as_uint(y[0]), __float_as_uint(y[1]),
                                                         __float_as_uint(y[2]), __float_as_uint(y[3])},
@@ -1173,6 +1175,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
             if (mrow < p.M) nssq[(int64_t)mrow * p.ssq_ld + gcol] = red[j];
           }
         }
+      }
+      if constexpr (MXO) {
+        const int xrow = row_of(r, b8 * 8 + (q & 7));
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)xkeep, rmxs, xrow * (int)(p.seg_n / 32) + (q >> 3), 0, 0);
       }
       // one batch of LDS reads live at a time
       __builtin_amdgcn_sched_barrier(0);
