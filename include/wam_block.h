@@ -184,7 +184,9 @@ int64_t wam_linear_workspace_bytes(int M, int N, int n_seg, int K);
 
 /* Per-row fp8 quantization of a bf16 matrix w [rows, cols] (row stride ldw):
  * scale[r] = max_c |w[r,c]| / 448 (1 for an all-zero row) and
- * q[r, c] = e4m3(w[r,c] / scale[r]), round to nearest even (q row stride cols).
+ * q[r, c] = e4m3(w[r,c] * (448 / max_c |w[r,c]|)) (fp32 product with the
+ * row's fp32 reciprocal factor; factor 1 for an all-zero row), round to
+ * nearest even (q row stride cols).
  * Prepares the fp8 weights of wam_linear (w_dtype = WAM_FP8).  No counterpart
  * in the reference, which has no fp8 path. */
 int wam_quantize_fp8_rows(const void* w, int rows, int cols, int64_t ldw, void* q, float* scale,
@@ -206,7 +208,8 @@ typedef struct {
   /* Optional e4m3 copy of y (no counterpart in the reference; the fp8
    * activations of wam_linear): y8 [rows, D] bytes and y8_scale [rows] fp32
    * with y8_scale[r] = max_d |y[r,d]| / 448 (1 for an all-zero row) and
-   * y8[r,d] = e4m3(y[r,d] / y8_scale[r]) rounded to nearest even, y being the
+   * y8[r,d] = e4m3(y[r,d] * (448 / max_d |y[r,d]|)) rounded to nearest even
+   * (as wam_quantize_fp8_rows), y being the
    * bf16 result (the same bytes wam_quantize_fp8_rows makes of it).  With y8
    * set, y may be NULL (no bf16 output). */
   void* y8; float* y8_scale;

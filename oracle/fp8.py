@@ -9,7 +9,8 @@ of the FFN unit replaces each weight W [N, K] by per-output-channel e4m3
 values with one fp32 scale per row:
 
   scale[n] = max_k |W[n, k]| / 448      (1 for an all-zero row)
-  q[n, k]  = e4m3fn(W[n, k] / scale[n])  round to nearest even, |q| <= 448
+  q[n, k]  = e4m3fn(W[n, k] * f[n])      round to nearest even, |q| <= 448
+  f[n]     = 448 / max_k |W[n, k]|       (fp32; 1 for an all-zero row)
 
 and computes with W' = q * scale (bf16 activations, fp32 accumulation).  The
 rounding is torch's float8_e4m3fn cast (OCP E4M3: 4 exponent bits, bias 7, 3
@@ -27,8 +28,12 @@ def quantize_rows(w):
     """w [N, K] (bf16 or fp32) -> (q [N, K] float8_e4m3fn, scale [N] fp32)."""
     wf = w.float()
     amax = wf.abs().amax(dim=1)
-    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
-    q = (wf / scale[:, None]).to(E4M3)
+    # true fp32 divisions by tensors (a Python scalar operand may be applied
+    # through a reciprocal, which rounds twice)
+    c448 = torch.full_like(amax, E4M3_MAX)
+    scale = torch.where(amax > 0, amax / c448, torch.ones_like(amax))
+    f = torch.where(amax > 0, c448 / amax, torch.ones_like(amax))
+    q = (wf * f[:, None]).to(E4M3)
     return q, scale
 
 

@@ -191,6 +191,18 @@ def test_fp8_quantization_pinned():
     # relative error of a normal e4m3 value is at most 2^-4 (3 mantissa bits, RNE)
     nz = w.abs() > 0
     assert ((deq - w).abs()[nz] <= w.abs()[nz] * 2 ** -4 + 1e-12).all()
+    # the factor 448 / max is one correctly rounded fp32 division, and the
+    # product is rounded to fp32 before the e4m3 rounding: -0.017578125 *
+    # fp32(448 / 3) is exactly -2.625 in fp32, a tie that goes to the even
+    # code -2.5 (with fp32(448 * fp32(1 / 3)) it would land on -2.75)
+    q, s = fp8.quantize_rows(torch.tensor([[-0.017578125, 3.0]]))
+    assert q.float()[0, 0].item() == -2.5 and q.float()[0, 1].item() == 448.0
+    amax = torch.rand(2000, generator=torch.Generator().manual_seed(3)) * 100 + 1e-3
+    w = torch.stack([amax, -amax / 3], dim=1)
+    q, s = fp8.quantize_rows(w)
+    f = (448.0 / amax.double()).float()
+    assert torch.equal(q.view(torch.uint8), (w * f[:, None]).to(fp8.E4M3).view(torch.uint8))
+    assert torch.equal(s, (amax.double() / 448.0).float())
 
 
 def test_mx32_quantization_pinned():

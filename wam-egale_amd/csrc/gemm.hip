@@ -1742,14 +1742,15 @@ __global__ __launch_bounds__(256) void quantize_fp8_rows_kernel(const bf16* __re
   __syncthreads();
   const float amax = __uint_as_float(smax);
   const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+  const float inv = amax > 0.f ? 448.0f / amax : 1.0f;  // one division per row
   uint8_t* qrow = q + (int64_t)r * cols;
   for (int c = tid * 8; c < cols; c += 256 * 8) {
     const bf16x8 v = ld_bf16x8(row + c);
     int lo = 0, hi = 0;
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[0]) / sc, static_cast<float>(v[1]) / sc, lo, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[2]) / sc, static_cast<float>(v[3]) / sc, lo, true);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[4]) / sc, static_cast<float>(v[5]) / sc, hi, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[6]) / sc, static_cast<float>(v[7]) / sc, hi, true);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[0]) * inv, static_cast<float>(v[1]) * inv, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[2]) * inv, static_cast<float>(v[3]) * inv, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[4]) * inv, static_cast<float>(v[5]) * inv, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(static_cast<float>(v[6]) * inv, static_cast<float>(v[7]) * inv, hi, true);
     *reinterpret_cast<u32x2*>(qrow + c) = u32x2{(unsigned)lo, (unsigned)hi};
   }
   if (tid == 0) scale[r] = sc;

@@ -54,7 +54,8 @@ __device__ inline void ln_coeffs(const wam_ln_args& a, int64_t row, int ch, floa
 }
 
 // Q8: the bf16 rows are also written as e4m3 with one fp32 scale per row,
-// scale = max |bf16 row| / 448 (1 for an all-zero row), q = e4m3(y / scale)
+// scale = max |bf16 row| / 448 (1 for an all-zero row), q = e4m3(y * (448 /
+// max)) (one division per row)
 // rounded to nearest even: what the row quantizer of the fp8 GEMM makes of
 // the bf16 output, without reading it back.
 template <int CH, bool XF32, bool Q8>
@@ -131,16 +132,17 @@ __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args 
   if (Q8) {
     const float amax = wave_max(mx);
     const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+    const float inv = amax > 0.f ? 448.0f / amax : 1.0f;
     uint8_t* q = static_cast<uint8_t*>(a.y8) + row * D;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       const int ch = lane + c * 64;
       if (ch >= nch) continue;
       int lo = 0, hi = 0;
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][0] / sc, v[c][1] / sc, lo, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][2] / sc, v[c][3] / sc, lo, true);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][4] / sc, v[c][5] / sc, hi, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][6] / sc, v[c][7] / sc, hi, true);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][0] * inv, v[c][1] * inv, lo, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][2] * inv, v[c][3] * inv, lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][4] * inv, v[c][5] * inv, hi, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[c][6] * inv, v[c][7] * inv, hi, true);
       *reinterpret_cast<u32x2*>(q + ch * 8) = u32x2{(unsigned)lo, (unsigned)hi};
     }
     if (lane == 0) a.y8_scale[row] = sc;

@@ -87,8 +87,8 @@ FP8 = torch.float8_e4m3fn
 
 
 def quantize_fp8_rows(w, out=None, scale=None):
-    """Per-row e4m3 weights: scale[r] = max|w[r]| / 448, q = e4m3(w / scale)
-    (round to nearest even).  Returns (q [rows, cols] float8_e4m3fn, scale fp32)."""
+    """Per-row e4m3 weights: scale[r] = max|w[r]| / 448, q = e4m3(w * (448 /
+    max|w[r]|)) (round to nearest even).  Returns (q [rows, cols] float8_e4m3fn, scale fp32)."""
     dev = _dev(w)
     _bf16(w, "w")
     _req(w.dim() == 2 and w.stride(-1) == 1, "w must be [rows, cols] with contiguous rows")
