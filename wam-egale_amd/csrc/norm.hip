@@ -55,9 +55,9 @@ __device__ inline void ln_coeffs(const wam_ln_args& a, int64_t row, int ch, floa
 
 // Q8: the bf16 rows are also written as e4m3 with one fp32 scale per row,
 // scale = max |bf16 row| / 448 (1 for an all-zero row), q = e4m3(y * (448 /
-// max)) (one division per row)
-// rounded to nearest even: what the row quantizer of the fp8 GEMM makes of
-// the bf16 output, without reading it back.
+// max)) rounded to nearest even (one division per row): what the row
+// quantizer of the fp8 GEMM makes of the bf16 output, without reading it
+// back.
 template <int CH, bool XF32, bool Q8>
 __global__ __launch_bounds__(64 * kLnWaves) void ln_modulate_kernel(wam_ln_args a) {
   __shared__ __attribute__((aligned(16))) float s_mul[kLnMaxD];
