@@ -572,7 +572,8 @@ __device__ __forceinline__ void w4_sched() {
   }
 }
 
-// RF32 / OF32: the residual / output is fp32 (else bf16); compile-time so
+// RF32 / OF32: the residual / output is fp32 (else bf16; OF32 = 2: e4m3 with
+// e8m0 exponents per 32 columns, the MX output); compile-time so
 // that the epilogue's loads and stores are branch-free.  TM: tile rows, 256
 // (waves 2 x 2, 128 x 128 each) or 224 (waves 1 x 4, 224 x 64 each).
 // WB: bytes per weight element, 2 (bf16) or 1 (fp8 e4m3 with per-column
@@ -584,7 +585,8 @@ __device__ __forceinline__ void w4_sched() {
 // product runs on v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales.  A
 // k-step is then 128 values = 128 bytes per row, so staging, LDS layout and
 // epilogue are those of bf16 byte for byte; only the fragment reads (32 bytes
-// per lane) and the MFMA differ.
+// per lane) and the MFMA differ.  AMX: A carries e8m0 exponents per row and
+// 32 k instead of a row scale, applied as the MFMA's block scales.
 template <int EPI, int RF32, int OF32, int TM, int WB = 2, bool F8MM = false, bool AMX = false>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
   static_assert(TM == 256 || TM == 224, "tile rows");
@@ -1603,6 +1605,8 @@ int linear(const wam_linear_args* a, hipStream_t s) {
   if (a8 || amx) {
     WAM_REQUIRE(f8 && (amx ? a->a_block_scale != nullptr : a->a_scale != nullptr),
                 "wam_linear: fp8 activations need fp8 weights and a_scale (a_block_scale for WAM_FP8_MX)");
+    WAM_REQUIRE(!amx || ((uintptr_t)a->a_block_scale & 3) == 0,
+                "wam_linear: a_block_scale must be 4-byte aligned (one word per row and 128 values)");
     if (a8)
       WAM_REQUIRE((a->epilogue == WAM_EPI_BIAS || a->epilogue == WAM_EPI_BIAS_GELU) && !norm,
                   "wam_linear: fp8 activations with row scales take WAM_EPI_BIAS or WAM_EPI_BIAS_GELU");
