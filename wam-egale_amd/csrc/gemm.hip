@@ -1232,29 +1232,49 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(LinearParams p)
   if (i >= (int64_t)p.M * q4) return;
   const int m = (int)(i / q4), n = (int)(i - (int64_t)m * q4) * 4;
   const int64_t plane = (int64_t)p.M * p.seg_n, at = (int64_t)m * p.seg_n + n;
-  f32x4 v = *reinterpret_cast<const f32x4*>(p.part + at);
-  for (int r = 1; r < p.k_split; ++r) v += *reinterpret_cast<const f32x4*>(p.part + r * plane + at);
-  float bv[4] = {0.f, 0.f, 0.f, 0.f}, wsc[4] = {1.f, 1.f, 1.f, 1.f};
-  if (p.bias[0]) {
-    const bf16x4 t = *reinterpret_cast<const bf16x4*>(p.bias[0] + n);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) bv[e] = static_cast<float>(t[e]);
-  }
+  // The loads are issued before any is used and none inside a branch whose
+  // body uses it (the compiler waits for such a load at the branch's end):
+  // the first two ranges (a split launch has at least two), the bias through
+  // a buffer resource (a null bias is a zero-length one: zeros), the scales
+  // and the residual's raw words; the adds and widening come after.
+  const f32x4 v0 = *reinterpret_cast<const f32x4*>(p.part + at);
+  const f32x4 v1 = *reinterpret_cast<const f32x4*>(p.part + plane + at);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias[0], p.bias[0] ? (uint32_t)p.seg_n * 2u : 0u);
+  const u32x2 braw = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rb, n * 2, 0, 0));
+  float wsc[4] = {1.f, 1.f, 1.f, 1.f};
   if constexpr (WB == 1) {
     const float4 t = *reinterpret_cast<const float4*>(p.wscale[0] + n);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
-  const float no_gate[4] = {0.f, 0.f, 0.f, 0.f};
-  float rv[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES) {
+  constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
+  u32x4 rraw = {0u, 0u, 0u, 0u};
+  if constexpr (RES) {
     const int64_t ro = (int64_t)m * p.ldr + n;
     if (p.res_f32) {
-      const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p.res) + ro);
-      rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
+      rraw = *reinterpret_cast<const u32x4*>(static_cast<const float*>(p.res) + ro);
     } else {
-      const bf16x4 t = *reinterpret_cast<const bf16x4*>(static_cast<const bf16*>(p.res) + ro);
+      const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const bf16*>(p.res) + ro);
+      rraw = u32x4{t[0], t[1], 0u, 0u};
+    }
+  }
+  f32x4 v = v0 + v1;
+  for (int r = 2; r < p.k_split; ++r) v += *reinterpret_cast<const f32x4*>(p.part + r * plane + at);
+  float bv[4];
+  bv[0] = __uint_as_float(braw[0] << 16);
+  bv[1] = __uint_as_float(braw[0] & 0xffff0000u);
+  bv[2] = __uint_as_float(braw[1] << 16);
+  bv[3] = __uint_as_float(braw[1] & 0xffff0000u);
+  const float no_gate[4] = {0.f, 0.f, 0.f, 0.f};
+  float rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (RES) {
+    if (p.res_f32) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) rv[e] = static_cast<float>(t[e]);
+      for (int e = 0; e < 4; ++e) rv[e] = __uint_as_float(rraw[e]);
+    } else {
+      rv[0] = __uint_as_float(rraw[0] << 16);
+      rv[1] = __uint_as_float(rraw[0] & 0xffff0000u);
+      rv[2] = __uint_as_float(rraw[1] << 16);
+      rv[3] = __uint_as_float(rraw[1] & 0xffff0000u);
     }
   }
   epi_apply<EPI, WB>(p, p.out[0], m, n, v, bv, wsc, no_gate, false, rv);

@@ -115,6 +115,7 @@ __device__ inline bf16x8 buf_ld16(__amdgpu_buffer_rsrc_t r, int voff) {
 }
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Eight OCP fp8 e4m3 values (bytes 0..7 of q) widened to bf16 (exact: every
@@ -220,19 +221,27 @@ __device__ inline void split_row(int64_t row, int tokens, int64_t& b, int64_t& t
   t = r - q * n;
 }
 
-// 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb,
-// for token row `row` (b = row / tokens, t = row % tokens).
-__device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[8]) {
-  if (dtype == WAM_F32) {
-    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + off);
-    const float4 a = q[0], c = q[1];
-    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-    out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
-  } else {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(p) + off);
+// fp32 values of 8 consecutive elements held as raw words: a and c are the
+// 8 fp32 values (f32), or a holds the 8 bf16 values (c unused).
+__device__ inline void widen8(bool f32, u32x4 a, u32x4 c, float out[8]) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = static_cast<float>(v[e]);
+  for (int e = 0; e < 4; ++e) {
+    const unsigned lo = a[e >> 1], hi = a[2 + (e >> 1)];
+    out[e] = __uint_as_float(f32 ? a[e] : ((e & 1) ? (lo & 0xffff0000u) : (lo << 16)));
+    out[4 + e] = __uint_as_float(f32 ? c[e] : ((e & 1) ? (hi & 0xffff0000u) : (hi << 16)));
   }
+}
+// 8 consecutive values p[off .. off+8) of a bf16 or fp32 vector, widened to
+// fp32.  Both 16-byte loads are issued whatever the dtype (for bf16 the
+// second repeats the first), so neither sits in a branch of its own: the
+// compiler waits for a load inside a branch before the branch ends, which
+// turns a run of such calls into one memory round trip each.
+__device__ inline void ld8_f32(const void* p, int dtype, int64_t off, float out[8]) {
+  const bool f32 = dtype == WAM_F32;
+  const char* base = static_cast<const char*>(p) + off * (f32 ? 4 : 2);
+  const u32x4 a = *reinterpret_cast<const u32x4*>(base);
+  const u32x4 c = *reinterpret_cast<const u32x4*>(base + (f32 ? 16 : 0));
+  widen8(f32, a, c, out);
 }
 // Row of temb that serves token row `row`: per sample, per token, or per
 // group of tokens / temb_len consecutive tokens (one latent frame).
@@ -248,6 +257,8 @@ __device__ inline int64_t temb_row(const wam_modulation& m, int64_t row) {
 __device__ inline int64_t temb_off(const wam_modulation& m, int64_t trow, int idx, int D, int d) {
   return m.temb_mods == 1 ? trow * D + d : (trow * 6 + idx) * (int64_t)D + d;
 }
+// 8 consecutive modulation values mod[b, t, idx, d .. d+8) = table + temb,
+// for token row `row` (b = row / tokens, t = row % tokens).
 __device__ inline void ld_mod8(const wam_modulation m, int D, int64_t row, int idx, int d, float out[8]) {
   float tb[8];
   ld8_f32(m.table, m.table_dtype, (int64_t)idx * D + d, out);
