@@ -110,6 +110,19 @@ def test_linear_epilogues(dev, M, K, N):
                    tokens=tokens, gate_index=5)
     r = res32 + ref * gate
     assert_close(y, r, _ulp_bound(r), 0.99999, "gated fp32 residual per-token")
+    # per-frame temb (one modulation row per group of consecutive tokens): long
+    # frames put one boundary in some row tiles (the two-row gate), short ones
+    # several (the per-row gate)
+    divs = [f for f in range(1, tokens + 1) if tokens % f == 0]
+    for frames in sorted({max(f for f in divs if f <= 4), min(divs, key=lambda f: abs(tokens // f - 130))}):
+        tembf = _randn((B, frames, 6, D), dev, 9 + frames, 0.1, torch.float32)
+        fr = (torch.arange(tokens, device=dev) // (tokens // frames)).repeat(B)
+        bi = torch.arange(M, device=dev) // tokens
+        gate = table[0, 2][None] + tembf[bi, fr, 2]
+        y = ops.linear(x, w, b, epilogue=ops.EPI_BIAS_GATE_RES, residual=res32, table=table, temb=tembf,
+                       tokens=tokens, gate_index=2, out_dtype=torch.float32)
+        r = res32 + ref * gate
+        assert_close(y, r, 1e-3, 0.999999, f"gated fp32 residual, {frames} frames per sample")
 
 
 def test_linear_rejects_bad_shapes(dev):

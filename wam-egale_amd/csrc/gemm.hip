@@ -226,7 +226,7 @@ __device__ __forceinline__ void epi_apply(const LinearParams& p, void* out, int 
   *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = o;
 }
 
-template <class C, int EPI>
+template <class C, int EPI, int RF32 = 0>
 __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(LinearParams p) {
   // One __shared__ object per pipeline stage: the compiler tracks the
   // direct-to-LDS loads per object, so reading one stage while another is
@@ -334,14 +334,6 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     const float4 t = n_ok ? *reinterpret_cast<const float4*>(ws + n) : make_float4(1.f, 1.f, 1.f, 1.f);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
-  // The gate of this lane's 4 columns, once per tile when all the tile's rows
-  // read the same modulation row (one sample, or one latent frame).
-  float gate[4] = {0.f, 0.f, 0.f, 0.f};
-  bool gate_once = false;
-  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + C::BM, p.M) - 1);
-    if (gate_once && n_ok) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
-  }
   f32x16 acc[C::TN][C::TM];
 #pragma unroll
   for (int j = 0; j < C::TN; ++j)
@@ -432,27 +424,53 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
   // low half), so the whole round's loads are in flight together.
   constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
   constexpr int ITERS = ROUND / (C::kWaves * RPI);
+  constexpr int RB = RF32 ? 4 : 2;  // residual bytes per element
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-  u32x4v rraw[RES ? ITERS : 1];
+  typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+  // The residual through a buffer resource over the tile's rows from column
+  // n0 (rows past M read zeros), so the prefetch has no branch: a load inside
+  // a branch, or a dtype chosen at run time, left the compiler waiting for
+  // all memory operations (the previous rows' stores included) before every
+  // row of the epilogue.
+  const int rows_left = min(p.M - m0, C::BM);
+  const __amdgpu_buffer_rsrc_t rres =
+      RES ? make_rsrc(static_cast<const char*>(p.res) + ((int64_t)m0 * p.ldr + n0) * RB,
+                      (uint32_t)((rows_left - 1) * (uint32_t)p.ldr + (uint32_t)min(C::BN, p.seg_n - n0)) * RB)
+          : make_rsrc(p.a, 0u);
+  std::conditional_t<RF32 != 0, u32x4v, u32x2v> rraw[RES ? ITERS : 1];
   auto res_prefetch = [&](int rd) {
     if constexpr (RES) {
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
-        const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;
-        const int row = rd * ROUND + rr;
-        const int m = m0 + row;
-        if (row >= C::BM || m >= p.M || !n_ok) continue;
-        const int64_t ro = (int64_t)m * p.ldr + n;
-        if (p.res_f32) {
-          rraw[it] = *reinterpret_cast<const u32x4v*>(static_cast<const float*>(p.res) + ro);
-        } else {
-          const u32x2 t = *reinterpret_cast<const u32x2*>(static_cast<const bf16*>(p.res) + ro);
-          rraw[it] = u32x4v{t[0], t[1], 0u, 0u};
-        }
+        const int row = rd * ROUND + (it * C::kWaves + wave) * RPI + lane / QPR;
+        const int off = (row * (int)p.ldr + 4 * q) * RB;
+        if constexpr (RF32)
+          rraw[it] = __builtin_bit_cast(u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rres, off, 0, 0));
+        else
+          rraw[it] = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rres, off, 0, 0));
       }
     }
   };
   res_prefetch(0);
+  // The gate of this lane's 4 columns, loaded once per tile (after the k
+  // loop, which has no registers to spare for it) when the tile's rows read
+  // at most two consecutive modulation rows (one or two samples, or latent
+  // frames): gate for the rows before gate_split, gate2 from there on.  Rows
+  // that read more (one modulation row per token) load theirs per row.
+  float gate[4] = {0.f, 0.f, 0.f, 0.f}, gate2[4] = {0.f, 0.f, 0.f, 0.f};
+  bool gate_held = false;
+  int gate_split = 0;  // first tile row served by the second modulation row
+  if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
+    const int m_last = min(m0 + C::BM, p.M) - 1;
+    const int64_t tr0 = temb_row(p.gate, m0), tr1 = temb_row(p.gate, m_last);
+    gate_held = tr1 - tr0 <= 1;
+    gate_split = (int)(temb_first_row(p.gate, tr1) - m0);
+    // columns clamped into the row: both loads unconditional, in flight with
+    // the residual's
+    const int nc = min(n, p.seg_n - 4) + p.n_off;
+    ld_mod4(p.gate, p.mod_d, m0, p.gate_index, nc, gate);
+    ld_mod4(p.gate, p.mod_d, m_last, p.gate_index, nc, gate2);
+  }
   // Every wave is done reading the last stage (its fragments are in
   // registers and consumed); only LDS operations are waited for, so the
   // residual loads stay in flight.
@@ -478,6 +496,9 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are done
     __builtin_amdgcn_s_barrier();
+    // the round's residual rows have landed (one wait per round, which also
+    // drains the previous round's stores)
+    if constexpr (RES) wait_vmcnt<0>();
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
@@ -492,8 +513,8 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       } else {
         float rv[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (RES) {
-          const u32x4v t = rraw[it];
-          if (p.res_f32) {
+          const auto t = rraw[it];
+          if constexpr (RF32) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) rv[e] = __uint_as_float(t[e]);  // by value: a vector element has no address
           } else {
@@ -503,7 +524,10 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
             rv[3] = __uint_as_float(t[1] & 0xffff0000u);
           }
         }
-        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gate, gate_once, rv);
+        float gsel[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gsel[e] = row >= gate_split ? gate2[e] : gate[e];
+        epi_apply<EPI, C::WB>(p, out, m, n, v, bv, wsc, gsel, gate_held, rv);
       }
     }
     if (rd + 1 < NROUNDS) {
@@ -907,11 +931,19 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
     const float4 t = *reinterpret_cast<const float4*>((seg == 0 ? p.wscale[0] : (seg == 1 ? p.wscale[1] : p.wscale[2])) + n);
     wsc[0] = t.x; wsc[1] = t.y; wsc[2] = t.z; wsc[3] = t.w;
   }
-  float gate[4] = {0.f, 0.f, 0.f, 0.f};
-  bool gate_once = false;
+  // The gate of the lane's 4 columns for the tile's rows when they read at
+  // most two consecutive modulation rows (samples or latent frames): gate
+  // before tile row gate_split, gate2 from there on; otherwise per row.
+  float gate[4] = {0.f, 0.f, 0.f, 0.f}, gate2[4] = {0.f, 0.f, 0.f, 0.f};
+  bool gate_held = false;
+  int gate_split = 0;
   if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
-    gate_once = temb_row(p.gate, m0) == temb_row(p.gate, min(m0 + TM, p.M) - 1);
-    if (gate_once) ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
+    const int m_last = min(m0 + TM, p.M) - 1;
+    const int64_t tr0 = temb_row(p.gate, m0), tr1 = temb_row(p.gate, m_last);
+    gate_held = tr1 - tr0 <= 1;
+    gate_split = (int)(temb_first_row(p.gate, tr1) - m0);
+    ld_mod4(p.gate, p.mod_d, m0, p.gate_index, n + p.n_off, gate);
+    ld_mod4(p.gate, p.mod_d, m_last, p.gate_index, n + p.n_off, gate2);
   }
   constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
   constexpr bool PART = EPI == kEpiPartial;
@@ -1106,9 +1138,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(LinearParams p) {
           }
           if constexpr (EPI == WAM_EPI_BIAS_GATE_RES) {
             float gt[4];
-            if (gate_once) {
+            if (gate_held) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) gt[e] = gate[e];
+              for (int e = 0; e < 4; ++e) gt[e] = row >= gate_split ? gate2[e] : gate[e];
             } else {
               // rows past M read the last row's modulation (their stores are dropped)
               ld_mod4(p.gate, p.mod_d, min(m0 + row, p.M - 1), p.gate_index, n + p.n_off, gt);
@@ -1344,7 +1376,11 @@ static void launch_tiles(dim3 grid, const LinearParams& p, hipStream_t s) {
       hipLaunchKernelGGL((gemm_w4_kernel<EPI, 0, 0, C::BM, C::WB>), grid, dim3(C::kThreads), 0, s, p);
     }
   } else {
-    hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI>), grid, dim3(C::kThreads), 0, s, p);
+    constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
+    if (RES && p.res_f32)
+      hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 1>), grid, dim3(C::kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 0>), grid, dim3(C::kThreads), 0, s, p);
   }
 }
 

@@ -253,6 +253,15 @@ __device__ inline int64_t temb_row(const wam_modulation& m, int64_t row) {
   const uint32_t group = (uint32_t)m.tokens / (uint32_t)m.temb_len;
   return b * m.temb_len + (uint32_t)t / group;
 }
+// First token row served by temb row `trow` (temb_row does not decrease
+// along the token rows, so row r is served by trow or a later row iff r >=
+// this).
+__device__ inline int64_t temb_first_row(const wam_modulation& m, int64_t trow) {
+  if (m.temb_len == 1) return trow * m.tokens;
+  if (m.temb_len == m.tokens) return trow;
+  const int64_t b = trow / m.temb_len, k = trow - b * m.temb_len;
+  return b * m.tokens + k * (m.tokens / m.temb_len);
+}
 // Element offset of temb[trow, idx, d]: [.., 6, D] rows, or one vector per row.
 __device__ inline int64_t temb_off(const wam_modulation& m, int64_t trow, int idx, int D, int d) {
   return m.temb_mods == 1 ? trow * D + d : (trow * 6 + idx) * (int64_t)D + d;
