@@ -77,13 +77,50 @@ __device__ inline long long block_reduce_ll(long long v, bool take_max, long lon
 
 // Thread t owns the contiguous slots [t * S, t * S + S) (S = ceil(P / 1024)),
 // so every list below is built in ascending slot order by one block scan over
-// per-thread counts, and each thread issues the loads of its slots together.
+// per-thread counts.  With MAXS > 0 (S <= MAXS) the thread reads its slots'
+// mask and ids once, all loads issued together, and keeps them in registers
+// through the passes (eviction rounds, next id, history list); read from
+// memory in every pass, each load sat in a branch of its own and cost one
+// round trip.  MAXS == 0 reads memory in every pass (pools beyond 1024 * the
+// largest MAXS).
+template <int MAXS>
 __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout_args a) {
   __shared__ int sh_i[kLayoutWaves];
   __shared__ long long sh_ll[kLayoutWaves];
   const int tid = threadIdx.x, P = a.pool;
   const int S = (P + kLayoutThreads - 1) / kLayoutThreads;
   const int lo = min(tid * S, P), hi = min(lo + S, P);
+  constexpr int NS = MAXS > 0 ? MAXS : 1;
+  uint8_t mreg[NS];
+  long long idreg[NS];
+  if constexpr (MAXS > 0) {
+#pragma unroll
+    for (int j = 0; j < MAXS; ++j) {
+      const int i = min(lo + j, P - 1);
+      mreg[j] = a.mask[i];
+      idreg[j] = (long long)a.ids[i];
+    }
+#pragma unroll
+    for (int j = 0; j < MAXS; ++j) mreg[j] = lo + j < hi ? mreg[j] : 0;
+  }
+  // slot lo + j of this thread (j < S): valid?  id?
+  auto valid = [&](int j) -> bool {
+    if constexpr (MAXS > 0) return mreg[j] != 0;
+    else return lo + j < hi && a.mask[lo + j] != 0;
+  };
+  auto id_of = [&](int j) -> long long {
+    if constexpr (MAXS > 0) return idreg[j];
+    else return (long long)a.ids[lo + j];
+  };
+  auto evict = [&](int j) {
+    if constexpr (MAXS > 0) {
+      mreg[j] = 0;
+      idreg[j] = -1;
+    }
+    a.mask[lo + j] = 0;
+    a.ids[lo + j] = -1;
+  };
+  const int NJ = MAXS > 0 ? MAXS : S;  // slots visited per thread (MAXS: unrolled, masked)
   int error = 0;
   if (a.candidate) {
     int bad = 0;
@@ -93,23 +130,24 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   } else {
     // Eviction of the oldest ids (allocate_slots).
     int nfree = 0;
-    for (int i = lo; i < hi; ++i) nfree += a.mask[i] ? 0 : 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) nfree += (lo + j < hi && !valid(j)) ? 1 : 0;
     int need = a.tokens - block_sum(nfree, sh_i);
     while (need > 0) {
       long long mn = 0x7fffffffffffffffLL;
-      for (int i = lo; i < hi; ++i)
-        if (a.mask[i] && (long long)a.ids[i] < mn) mn = (long long)a.ids[i];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (valid(j) && id_of(j) < mn) mn = id_of(j);
       mn = block_reduce_ll(mn, false, sh_ll);
       int f = 0;
-      for (int i = lo; i < hi; ++i) f += (a.mask[i] && a.ids[i] == mn) ? 1 : 0;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) f += (valid(j) && id_of(j) == mn) ? 1 : 0;
       int tot;
       int pos = block_excl_scan(f, sh_i, &tot);
-      for (int i = lo; i < hi; ++i) {
-        if (a.mask[i] && a.ids[i] == mn) {
-          if (pos < need) {
-            a.mask[i] = 0;
-            a.ids[i] = -1;
-          }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (valid(j) && id_of(j) == mn) {
+          if (pos < need) evict(j);
           ++pos;
         }
       }
@@ -125,16 +163,18 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   long long next = -1;
   if (!a.candidate) {
     long long mx = -1;
-    for (int i = lo; i < hi; ++i)
-      if (a.mask[i] && (long long)a.ids[i] > mx) mx = (long long)a.ids[i];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (valid(j) && id_of(j) > mx) mx = id_of(j);
     next = block_reduce_ll(mx, true, sh_ll) + 1;
   }
   // History list and new slots, both in ascending slot order.
   int nv = 0, nf = 0;
-  for (int i = lo; i < hi; ++i) {
-    const int valid = a.mask[i] ? 1 : 0;
-    nv += valid;
-    nf += (!a.candidate && !valid) ? 1 : 0;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const bool in = lo + j < hi, v = valid(j);
+    nv += v ? 1 : 0;
+    nf += (!a.candidate && in && !v) ? 1 : 0;
   }
   int tv, tf;
   int pv = block_excl_scan(nv, sh_i, &tv);
@@ -142,17 +182,21 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   // Is the history one run of consecutive slots?  (Its first and last valid
   // slots, before this call's new slots are marked.)
   long long first = 0x7fffffffffffffffLL, lastv = -1;
-  for (int i = lo; i < hi; ++i)
-    if (a.mask[i]) {
-      first = min(first, (long long)i);
-      lastv = max(lastv, (long long)i);
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (valid(j)) {
+      first = min(first, (long long)(lo + j));
+      lastv = max(lastv, (long long)(lo + j));
     }
   first = block_reduce_ll(first, false, sh_ll);
   lastv = block_reduce_ll(lastv, true, sh_ll);
-  for (int i = lo; i < hi; ++i) {
-    const bool valid = a.mask[i];
-    if (valid) a.hist_slots[pv++] = i;
-    if (!a.candidate && !valid) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int i = lo + j;
+    if (i >= hi) continue;
+    const bool v = valid(j);
+    if (v) a.hist_slots[pv++] = i;
+    if (!a.candidate && !v) {
       if (pf < a.tokens) {
         a.new_slots[pf] = i;
         a.mask[i] = a.update != 0 ? 1 : 0;
@@ -184,7 +228,10 @@ int kv_layout(const wam_kv_layout_args* a, hipStream_t s) {
     WAM_REQUIRE(a->tokens >= 1 && a->tokens <= a->pool,
                 "wam_kv_layout: %d new tokens do not fit a pool of %d slots", a->tokens, a->pool);
   }
-  hipLaunchKernelGGL(kv_layout_kernel, dim3(1), dim3(kLayoutThreads), 0, s, *a);
+  const int S = (a->pool + kLayoutThreads - 1) / kLayoutThreads;
+  if (S <= 8) hipLaunchKernelGGL(kv_layout_kernel<8>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
+  else if (S <= 16) hipLaunchKernelGGL(kv_layout_kernel<16>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
+  else hipLaunchKernelGGL(kv_layout_kernel<0>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
   WAM_LAUNCHED("kv_layout_kernel");
   return WAM_OK;
 }
