@@ -187,12 +187,13 @@ def test_rms_rope(dev, B, M, H):
 # [2, tokens, 1, 64] table whose two samples differ (row m reads table row m,
 # no modulo), on the fused four-wave path (4680 rows) and on the norm pass
 # (520 rows).  6240 rows, one segment: one round of 320-row tiles and the
-# norm pass.
+# norm pass (with RoPE), or the 320-row kernel's own norm epilogue (without;
+# 6000 rows end in a 240-row tile).
 @pytest.mark.parametrize("M,nseg,grid", [(4680, 3, (6, 26, 30)), (4680, 1, None), (520, 3, (2, 10, 26)),
                                          (120, 1, (2, 6, 10)), (6240, 3, (2, 26, 30)),
                                          (4680, 3, (1, 12, 15)), (5120, 1, (5, 32, 32)),
                                          (4680, 1, "per-sample"), (520, 1, "per-sample"),
-                                         (6240, 1, (2, 26, 30))])
+                                         (6240, 1, (2, 26, 30)), (6240, 1, None), (6000, 1, None)])
 def test_linear_qk_norm(dev, M, nseg, grid):
     from wam_ops import ops, synthetic
     K = N = 3072

@@ -35,7 +35,7 @@ int rms_rope(const wam_rms_rope_args*, hipStream_t);
 int attention(const wam_attention_args*, hipStream_t);
 int64_t attention_workspace_bytes(int B, int Mq, int H, int64_t max_keys);
 int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K);
-bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes);
+bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes, bool rope);
 int kv_layout(const wam_kv_layout_args*, hipStream_t);
 int kv_commit(const wam_kv_commit_args*, hipStream_t);
 
@@ -253,13 +253,14 @@ static int block_forward(const wam_block_args* a, hipStream_t s) {
   const size_t rowb = (size_t)R * D * 2;
   // Cross-attention query norm: the projection's epilogue writes y g and the
   // row's sums of squares, attention applies 1/rms (no row pass), when the
-  // projection runs as one four-wave launch; other tilings would run the
-  // norm as a pass anyway, and the row pass is as fast.  A debug call runs
+  // projection runs as one launch of the four-wave kernel or as one round of
+  // 320-row tiles (6240 rows); other tilings would run the norm as a pass
+  // anyway, and the row pass is as fast.  A debug call runs
   // the same kernels; its copies of the projection (before the norm) and of
   // the normalised queries come from extra debug-only launches.  (For the
   // self-attention queries the same fusion measured even: the QKV
   // epilogue's cost matched the half of the q/k row pass it removes.)
-  const bool qnorm_fused = linear_norm_in_epilogue(R, D, 1, D, split_bytes);
+  const bool qnorm_fused = linear_norm_in_epilogue(R, D, 1, D, split_bytes, false);
   const int qparts = (D + 255) / 256;
 
   wam_modulation mod = a->mod;

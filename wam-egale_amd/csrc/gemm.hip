@@ -53,7 +53,7 @@ struct LinearParams {
 };
 
 constexpr int kEpiPartial = 100;   // kernel epilogue of a split-K range: raw fp32 sums
-constexpr int kEpiBiasNorm = 101;  // bias, then the q/k-norm epilogue (four-wave kernel only)
+constexpr int kEpiBiasNorm = 101;  // bias, then the q/k-norm epilogue (four-wave kernel; eight-wave without RoPE)
 
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int STAGES_, int BLOCKS_ = 1, int SCHED_ = 0,
           int WB_ = 2, int SPLIT_ = 1>
@@ -471,6 +471,20 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
     ld_mod4(p.gate, p.mod_d, m0, p.gate_index, nc, gate);
     ld_mod4(p.gate, p.mod_d, m_last, p.gate_index, nc, gate2);
   }
+  // q-norm epilogue (no RoPE here): the gamma of the lane's 4 columns and the
+  // segment's sums-of-squares array.  With 256-column tiles a wave holds one
+  // whole row of the tile per pass, so a row's sum is one wave reduction.
+  constexpr bool NORM = EPI == kEpiBiasNorm;
+  static_assert(!NORM || C::BN == 256, "the q-norm epilogue needs 256-column tiles");
+  float gm[4] = {1.f, 1.f, 1.f, 1.f};
+  float* nssq = nullptr;
+  if constexpr (NORM) {
+    nssq = seg == 0 ? p.ssq[0] : (seg == 1 ? p.ssq[1] : p.ssq[2]);
+    const bf16* g = seg == 0 ? p.ngamma[0] : (seg == 1 ? p.ngamma[1] : p.ngamma[2]);
+    const bf16x4 tg = *reinterpret_cast<const bf16x4*>(g + min(n, p.seg_n - 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gm[e] = static_cast<float>(tg[e]);
+  }
   // Every wave is done reading the last stage (its fragments are in
   // registers and consumed); only LDS operations are waited for, so the
   // residual loads stay in flight.
@@ -504,6 +518,29 @@ __global__ __launch_bounds__(C::kThreads, C::BLOCKS) void gemm_bf16_kernel(Linea
       const int rr = (it * C::kWaves + wave) * RPI + lane / QPR;  // row within the round
       const int row = rd * ROUND + rr;
       const int m = m0 + row;
+      if constexpr (NORM) {
+        // y = bf16(acc + b) as the bias epilogue rounds it; the row's sum of
+        // y^2 over the tile's 256 columns (every lane of the wave takes part
+        // in the reduction); the stored value bf16(y * gamma), one rounding.
+        const bool row_ok = row < C::BM && m < p.M;
+        const int lrr = rr % RPO;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(WAM_GEMM_BUF(rr / RPO) + lrr * ROW_B + ((q ^ (lrr & 15)) << 4));
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = static_cast<bf16>(v[e] + bv[e]);
+        const bf16x2 o01 = {o[0], o[1]}, o23 = {o[2], o[3]};
+        const float ss = __builtin_amdgcn_fdot2_f32_bf16(o23, o23, __builtin_amdgcn_fdot2_f32_bf16(o01, o01, 0.f, false),
+                                                         false);
+        const float tot = wave_sum(row_ok && n_ok ? ss : 0.f);
+        if (row_ok && lane == 0) nssq[(int64_t)m * p.ssq_ld + (n0 >> 8)] = tot;
+        if (row_ok && n_ok) {
+          bf16x4 t;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t[e] = static_cast<bf16>(static_cast<float>(o[e]) * gm[e]);
+          *reinterpret_cast<bf16x4*>(static_cast<bf16*>(out) + (int64_t)m * p.ldo + n) = t;
+        }
+        continue;
+      }
       if (row >= C::BM || m >= p.M || !n_ok) continue;
       const int obj = rr / RPO, lr = rr % RPO;
       const char* buf = WAM_GEMM_BUF(obj);
@@ -1377,10 +1414,13 @@ static void launch_tiles(dim3 grid, const LinearParams& p, hipStream_t s) {
     }
   } else {
     constexpr bool RES = EPI == WAM_EPI_BIAS_GATE_RES || EPI == WAM_EPI_BIAS_RES;
-    if (RES && p.res_f32)
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 1>), grid, dim3(C::kThreads), 0, s, p);
-    else
-      hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 0>), grid, dim3(C::kThreads), 0, s, p);
+    if constexpr (RES) {
+      if (p.res_f32) {
+        hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 1>), grid, dim3(C::kThreads), 0, s, p);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((gemm_bf16_kernel<C, EPI, 0>), grid, dim3(C::kThreads), 0, s, p);
   }
 }
 
@@ -1420,8 +1460,12 @@ static int launch_gemm(LinearParams& p, hipStream_t s) {
   }
   switch (p.epi) {
     case kEpiBiasNorm:
-      if constexpr (C::kW4) launch_tiles<C, kEpiBiasNorm>(dim3(grid), p, s);
-      else WAM_REQUIRE(false, "wam_linear: the q/k-norm epilogue runs in the four-wave kernel only");
+      if constexpr (C::kW4 || std::is_same_v<C, Cfg320x256w8>) {
+        WAM_REQUIRE(C::kW4 || p.nfreq == nullptr, "wam_linear: the 320-row q-norm epilogue has no RoPE");
+        launch_tiles<C, kEpiBiasNorm>(dim3(grid), p, s);
+      } else {
+        WAM_REQUIRE(false, "wam_linear: the q/k-norm epilogue runs in the four-wave or the 320-row kernel only");
+      }
       break;
     case WAM_EPI_BIAS:
       launch_tiles<C, WAM_EPI_BIAS>(dim3(grid), p, s);
@@ -1558,13 +1602,15 @@ int64_t linear_workspace_bytes(int M, int seg_n, int n_seg, int K) {
   return plan_workspace(gemm_plan(M, seg_n, n_seg, K, device_cu_count(), INT64_MAX), M, seg_n);
 }
 
-// Whether linear() applies the q/k-norm epilogue inside a single four-wave
-// launch for this bf16 shape (otherwise it runs the GEMM and then the norm
-// pass, which costs about what a separate RMSNorm pass costs).
-bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes) {
+// Whether linear() applies the q/k-norm epilogue inside its one launch for
+// this bf16 shape: the four-wave kernel, or one round of 320-row tiles when
+// there is no RoPE (otherwise it runs the GEMM and then the norm pass, which
+// costs about what a separate RMSNorm pass costs).
+bool linear_norm_in_epilogue(int M, int seg_n, int n_seg, int K, int64_t ws_bytes, bool rope) {
   if (M < 1 || K % 64 != 0 || !uses_big_tiles(M, seg_n, n_seg)) return false;
   const int cus = device_cu_count();
   if (w4_t224_wins(M, seg_n, n_seg, K, cus, ws_bytes)) return true;
+  if (t320_one_round(M, seg_n, n_seg, K, cus, ws_bytes)) return !rope;
   return gemm_plan(M, seg_n, n_seg, K, cus, ws_bytes).kind == 0;
 }
 
@@ -1735,6 +1781,10 @@ int linear(const wam_linear_args* a, hipStream_t s) {
       return launch_gemm<CfgW4t224>(p, s);
     }
     if (t320_one_round(a->M, a->seg_n, a->n_seg, a->K, device_cu_count(), ws_bytes)) {
+      if (norm && !p.nfreq) {
+        p.epi = kEpiBiasNorm;
+        return launch_gemm<Cfg320x256w8>(p, s);
+      }
       WAM_TRY(launch_gemm<Cfg320x256w8>(p, s));
       return norm ? linear_norm_pass(p, s) : WAM_OK;
     }
