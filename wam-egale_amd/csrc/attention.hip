@@ -654,19 +654,22 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
         for (int v = 0; v < 16; ++v)
           if (kt * 32 + 8 * (v >> 2) + (v & 3) >= thr) s[kt][v] = -INFINITY;
     }
-    float mq[4];
+    // The tile max of a lane's 32 scores as a tree of three-input maxima
+    // (16 v_maximum3: ten over triples, then the partial maxima), written
+    // so; pairs of two-input maxima came out as v_maximum3 with a repeated
+    // operand (27 per tile).
+    auto mx3 = [](float a, float b, float c) {
+      return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+    };
+    float t[11];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const f32x16& x = s[c >> 1];
-      const int o8 = (c & 1) * 8;
-      float m = __builtin_elementwise_maximum(x[o8], x[o8 + 1]);
-#pragma unroll
-      for (int v = 2; v < 8; v += 2)
-        m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(x[o8 + v], x[o8 + v + 1]));
-      mq[c] = m;
+    for (int i = 0; i < 10; ++i) {
+      const int k0 = 3 * i, k1 = 3 * i + 1, k2 = 3 * i + 2;
+      t[i] = mx3(s[k0 >> 4][k0 & 15], s[k1 >> 4][k1 & 15], s[k2 >> 4][k2 & 15]);
     }
-    const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(mq[0], mq[1]),
-                                                   __builtin_elementwise_maximum(mq[2], mq[3]));
+    t[10] = __builtin_elementwise_maximum(s[1][14], s[1][15]);
+    const float u0 = mx3(t[0], t[1], t[2]), u1 = mx3(t[3], t[4], t[5]), u2 = mx3(t[6], t[7], t[8]);
+    const float mx = mx3(mx3(u0, u1, u2), t[9], t[10]);
     const float mt = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64)) * sc;
     const bool grow = mt > m_run + 8.0f;
     const float m_new = grow ? mt : m_run;
