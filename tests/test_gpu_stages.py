@@ -176,6 +176,23 @@ def test_rms_rope(dev, B, M, H):
     assert_close(q2, ref, _ulp_bound(ref), 0.99999, "rms in place")
 
 
+def test_rms_rope_head_size_not_dividing_512(dev):
+    """Heads of 96 (a lane's chunks, 512 columns apart, sit at different
+    places in their heads): the rotation factors are read per chunk."""
+    from wam_ops import ops
+    B, M, hd, H = 2, 60, 96, 16
+    D = H * hd
+    x = _randn((B, M, D), dev, 1, 2.0)
+    g = _randn((D,), dev, 3, 0.02) + 1
+    gen = torch.Generator(device=dev).manual_seed(5)
+    ang = torch.rand((B, M, 1, hd // 2), generator=gen, device=dev) * 6.283
+    freq = torch.polar(torch.ones_like(ang), ang).contiguous()
+    (y,) = ops.rms_rope([x], [g], [1e-6], freq=freq, head_dim=hd)
+    n = torch.nn.functional.rms_norm(x.float(), (D,), g.float(), 1e-6).reshape(B, M, H, hd // 2, 2)
+    rot = torch.view_as_real(torch.view_as_complex(n.contiguous()) * freq).reshape(B, M, D)
+    assert_close(y, rot, _ulp_bound(rot), 0.99999, "rms+rope, 96-wide heads")
+
+
 # The q/k-norm epilogue of the projection: checked against the plain bias
 # GEMM's own bf16 output y (same kernels, same accumulation), so both the
 # sums of squares and bf16(rope(y * gamma)) have exact references.  4680
