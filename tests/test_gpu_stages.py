@@ -434,7 +434,7 @@ def _cache_pair(P, H, seed, dev, prefix_chunks):
     (100, [(40, 2), (40, 2)], 40, 2),      # evicts 20 of the oldest chunk
     (64, [(32, 2), (32, 1)], 48, 1),       # evicts a whole chunk and part of the next
     (3000, [(1000, 2), (1000, 1), (900, 2)], 1000, 0),
-    (12000, [(5000, 2), (4000, 1), (2500, 2)], 1500, 1),   # 12 slots per thread, evicts
+    (12000, [(5000, 2), (4000, 1), (2500, 2)], 1500, 1),   # 12 slots per thread (read per pass), evicts
     (20000, [(9000, 2), (9000, 1)], 3000, 2),               # 20 slots per thread (read per pass), evicts
 ])
 def test_kv_layout_matches_oracle(dev, P, chunks, tokens, update):

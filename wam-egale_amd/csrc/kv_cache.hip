@@ -81,8 +81,8 @@ __device__ inline long long block_reduce_ll(long long v, bool take_max, long lon
 // mask and ids once, all loads issued together, and keeps them in registers
 // through the passes (eviction rounds, next id, history list); read from
 // memory in every pass, each load sat in a branch of its own and cost one
-// round trip.  MAXS == 0 reads memory in every pass (pools beyond 1024 * the
-// largest MAXS).
+// round trip.  MAXS == 0 reads memory in every pass (pools beyond 8192
+// slots: 16 slots per thread in registers spilled).
 template <int MAXS>
 __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout_args a) {
   __shared__ int sh_i[kLayoutWaves];
@@ -90,22 +90,24 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   const int tid = threadIdx.x, P = a.pool;
   const int S = (P + kLayoutThreads - 1) / kLayoutThreads;
   const int lo = min(tid * S, P), hi = min(lo + S, P);
+  static_assert(MAXS <= 32, "the valid flags are bits of one word");
   constexpr int NS = MAXS > 0 ? MAXS : 1;
-  uint8_t mreg[NS];
+  uint32_t mbits = 0;  // bit j: slot lo + j is valid
   long long idreg[NS];
   if constexpr (MAXS > 0) {
+    uint8_t mreg[MAXS];
 #pragma unroll
-    for (int j = 0; j < MAXS; ++j) {
-      const int i = min(lo + j, P - 1);
-      mreg[j] = a.mask[i];
-      idreg[j] = (long long)a.ids[i];
+    for (int j = 0; j < MAXS; ++j) mreg[j] = a.mask[min(lo + j, P - 1)];
+    if (!a.candidate) {
+#pragma unroll
+      for (int j = 0; j < MAXS; ++j) idreg[j] = (long long)a.ids[min(lo + j, P - 1)];
     }
 #pragma unroll
-    for (int j = 0; j < MAXS; ++j) mreg[j] = lo + j < hi ? mreg[j] : 0;
+    for (int j = 0; j < MAXS; ++j) mbits |= (lo + j < hi && mreg[j] != 0) ? 1u << j : 0u;
   }
   // slot lo + j of this thread (j < S): valid?  id?
   auto valid = [&](int j) -> bool {
-    if constexpr (MAXS > 0) return mreg[j] != 0;
+    if constexpr (MAXS > 0) return (mbits >> j) & 1u;
     else return lo + j < hi && a.mask[lo + j] != 0;
   };
   auto id_of = [&](int j) -> long long {
@@ -114,20 +116,74 @@ __global__ __launch_bounds__(kLayoutThreads) void kv_layout_kernel(wam_kv_layout
   };
   auto evict = [&](int j) {
     if constexpr (MAXS > 0) {
-      mreg[j] = 0;
+      mbits &= ~(1u << j);
       idreg[j] = -1;
     }
     a.mask[lo + j] = 0;
     a.ids[lo + j] = -1;
   };
   const int NJ = MAXS > 0 ? MAXS : S;  // slots visited per thread (MAXS: unrolled, masked)
-  int error = 0;
   if (a.candidate) {
+    // Read only (candidate verification): the history list and its summary
+    // in one block pass: per wave a scan of the threads' valid counts and
+    // the minimum / maximum valid slot and the row check, then one exchange
+    // through LDS (the general path below runs five block scans and
+    // reductions for the same results).
+    __shared__ int sh_c[kLayoutWaves][4];
+    const int lane = tid & 63, w = tid >> 6;
     int bad = 0;
     for (int b = tid; b < a.batch; b += kLayoutThreads)
       bad |= (a.rows[b] < 0 || a.rows[b] >= a.pool_batch);
-    if (block_sum(bad, sh_i) != 0) error = 2;
-  } else {
+    int nv = 0, first = 0x7fffffff, lastv = -1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (valid(j)) {
+        ++nv;
+        first = min(first, lo + j);
+        lastv = max(lastv, lo + j);
+      }
+    int x = nv;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      first = min(first, __shfl_xor(first, o, 64));
+      lastv = max(lastv, __shfl_xor(lastv, o, 64));
+      bad |= __shfl_xor(bad, o, 64);
+    }
+    const int wave_total = __shfl(x, 63, 64);
+    if (lane == 0) {
+      sh_c[w][0] = wave_total;
+      sh_c[w][1] = first;
+      sh_c[w][2] = lastv;
+      sh_c[w][3] = bad;
+    }
+    __syncthreads();
+    int off = 0, tv = 0, bf = 0x7fffffff, bl = -1, bb = 0;
+#pragma unroll
+    for (int i = 0; i < kLayoutWaves; ++i) {
+      off += i < w ? sh_c[i][0] : 0;
+      tv += sh_c[i][0];
+      bf = min(bf, sh_c[i][1]);
+      bl = max(bl, sh_c[i][2]);
+      bb |= sh_c[i][3];
+    }
+    int pv = off + x - nv;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (valid(j)) a.hist_slots[pv++] = lo + j;
+    if (tid == 0) {
+      a.info[0] = tv;
+      a.info[1] = bb ? 2 : 0;
+      a.info[2] = (tv > 0 && bl - bf + 1 == tv) ? bf : -1;
+    }
+    return;
+  }
+  int error = 0;
+  {
     // Eviction of the oldest ids (allocate_slots).
     int nfree = 0;
 #pragma unroll
@@ -230,7 +286,6 @@ int kv_layout(const wam_kv_layout_args* a, hipStream_t s) {
   }
   const int S = (a->pool + kLayoutThreads - 1) / kLayoutThreads;
   if (S <= 8) hipLaunchKernelGGL(kv_layout_kernel<8>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
-  else if (S <= 16) hipLaunchKernelGGL(kv_layout_kernel<16>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
   else hipLaunchKernelGGL(kv_layout_kernel<0>, dim3(1), dim3(kLayoutThreads), 0, s, *a);
   WAM_LAUNCHED("kv_layout_kernel");
   return WAM_OK;
