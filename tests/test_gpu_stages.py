@@ -64,12 +64,13 @@ def test_linear_bias(dev, M, K, N, nseg):
 # tiles; the last one of 4500 holds 20 rows, over 65 k-tiles), every
 # epilogue included.  (6240, 6144, 3072), (6240, 3072, 3072) and (6000,
 # 1024, 3072) run as one round of 320-row tiles (the last one of 6000 holds
-# 240 rows).
+# 240 rows).  (6240, 3072, 14336) is the verify layer's FFN1: 51 column
+# tiles of 256-row tiles and the last 5 as a split-K tail in 2 ranges.
 @pytest.mark.parametrize("M,K,N", [(130, 1024, 2048), (4680, 1024, 2048), (4680, 256, 3584),
                                    (4680, 256, 14336), (6240, 3072, 2816), (6240, 6144, 3072),
                                    (3900, 4160, 4352), (300, 512, 200), (4680, 3072, 3072),
                                    (4680, 14336, 3072), (4500, 4160, 3072), (6240, 3072, 3072),
-                                   (6000, 1024, 3072)])
+                                   (6000, 1024, 3072), (6240, 3072, 14336)])
 def test_linear_epilogues(dev, M, K, N):
     from wam_ops import ops
     D = N
