@@ -377,8 +377,8 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 
 // ---------------------------------------------------------------------------
 // Software-pipelined variant for calls whose keys are all this call's own
-// (no KV pool): 8 waves x 32 queries, key tiles of 64 in 3 LDS stages.  Per
-// tile t a wave issues
+// (no KV pool): 8 waves x 32 queries, key tiles of 64 in 3 LDS stages (4
+// with PP below).  Per tile t a wave issues
 //   g1: S(t+1) = K_{t+1} Q^T (16 MFMAs)  interleaved with  softmax of S(t)
 //   g2: O += V_t^T P(t)     (16 MFMAs)
 // so the exponentials, row sums and bf16 packing of one tile run under the
@@ -389,14 +389,33 @@ __global__ __launch_bounds__(64 * W, 1) void attention_kernel(wam_attention_args
 // loads straight to LDS (rows past Mk read zeros) and Q through buffer loads
 // into registers.  Lane layouts of S^T, P and O^T are those of
 // attention_kernel.
-template <bool HIST, int NW>
+//
+// PP (ping-pong, for long key ranges): the two waves of a SIMD run half a
+// tile apart, so that one wave's softmax (VALU) runs beside the other's
+// O += V^T P MFMAs instead of beside its own S MFMAs only.  A workgroup's
+// waves land on the SIMDs in turn (wave w and w + 4 share one), so waves
+// 0-3 form group A and the others group B.  Both run the same sequence per
+// tile t, S(t+1) + softmax(t), then O += V_t P(t), with one barrier per tile:
+// A's after its softmax, B's after its P V, and B one barrier behind A from
+// the start.  Between two barriers A does P V(t) and S/softmax(t+1) while B
+// does S/softmax(t) and P V(t).  Tile t+3 is issued right after barrier t
+// into the stage of tile t-1 (four stages) and has landed by barrier t+1.
+// Same arithmetic per wave as the one-phase schedule, so the results are
+// identical; 4680 x 4680, 24 heads: 290-291 -> 273-275 us in the block.
+// With 8 key tiles (cross attention over 512 keys) it measured 1-3% slower,
+// so the host only picks it for long key ranges, and with pool keys (the
+// 4 x 1560-query verify layer over 7800 keys) the layer took 15-30 us longer,
+// so the pool path keeps one phase per tile.
+template <bool HIST, int NW, bool PP>
 __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_args a, const int* __restrict__ slots,
                                                                   int n_full, int n_split, float* __restrict__ part) {
   static_assert(NW == 8 || (NW == 7 && !HIST), "8 waves, or 7 without pool keys");
-  // three K/V stages, then (pool keys only) the 64 slots of each stage's
-  // tile, then each wave's query partial sums of squares (q_ssq)
+  static_assert(!(PP && HIST), "ping-pong without pool keys");
+  // K/V stages (three, four with PP), then (pool keys only) the 64 slots of
+  // each stage's tile, then each wave's query partial sums of squares (q_ssq)
+  constexpr int NST = PP ? 4 : 3;
   constexpr int kQpSlots = kQssqMax / 2;  // direct-to-LDS dword loads per wave: 2 partials each
-  constexpr int kQpOff = 3 * kAttnStage + (HIST ? 3 * kAttnKT * 4 : 0);
+  constexpr int kQpOff = NST * kAttnStage + (HIST ? NST * kAttnKT * 4 : 0);
   __shared__ __attribute__((aligned(1024))) char lds[kQpOff + NW * kQpSlots * 256];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -473,7 +492,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   const int nsub = (32 - wave + NW - 1) / NW;
   const int lr = lane >> 4, pch = lane & 15;
   // Slot list of the tile bound for stage st_bytes (64 ints).
-  auto slot_list = [&](int st_bytes) { return lds + 3 * kAttnStage + (st_bytes >> 15) * (kAttnKT * 4); };
+  auto slot_list = [&](int st_bytes) { return lds + NST * kAttnStage + (st_bytes >> 15) * (kAttnKT * 4); };
   static_assert(kAttnStage == 1 << 15, "stage index is st_bytes >> 15");
   // The last wave (one of those with the fewest sub-blocks) copies the 64
   // slots of tile T into the list of its stage: lane L slot T*64 + L.
@@ -554,32 +573,35 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
 
   // Per-lane LDS offsets inside a stage, computed once.  K fragment (kt, ks):
   // key kt*32 + l32, chunk 2 ks + half under the (key & 15) swizzle, i.e.
-  // kofs[ks] + 8192 kt.  Transposed V fragment (dt, ks), part pt: key 16 ks
-  // + 4 half + 8 pt + (lane % 16) / 4, d = 32 dt + 16 ((lane / 16) % 2) +
-  // 4 (lane % 4); with the V swizzle that is vofs[dt] + 4096 ks + 2048 pt.
-  int kofs[8], vofs[4];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) kofs[ks] = l32 * 256 + (((2 * ks + half) ^ (l32 & 15)) << 4);
+  // l32*256 + ((2 ks + half) ^ (l32 & 15)) * 16 + 8192 kt.  Bits 5-7 of that
+  // offset are 32 (ks ^ ((l32 & 15) >> 1)) and no other term touches them, so
+  // it is kofs0 ^ (32 ks) with kofs0 the ks = 0 offset (and a stage base,
+  // a multiple of 32 KB, adds without touching them either).  Transposed V
+  // fragment (dt, ks), part pt: key 16 ks + 4 half + 8 pt + (lane % 16) / 4,
+  // d = 32 dt + 16 ((lane / 16) % 2) + 4 (lane % 4); with the V swizzle that
+  // is vlane + 64 (dt ^ xs) + 4096 ks + 2048 pt, where 64 (dt ^ xs) alone sets
+  // bits 6-7: vofs0 ^ (64 dt).  Two registers instead of twelve.
+  const int kofs0 = l32 * 256 + ((half ^ (l32 & 15)) << 4);
+  int vofs0;
   {
     const int xs = tr_i >> 2, low = 2 * tr_gh + ((tr_i & 3) >> 1);
-    const int vlane = kAttnTile + (4 * half + xs) * 256 + (low << 4) + 8 * (tr_i & 1);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) vofs[dt] = vlane + 64 * (dt ^ xs);
+    vofs0 = kAttnTile + (4 * half + xs) * 256 + (low << 4) + 8 * (tr_i & 1) + 64 * xs;
   }
   // S = K Q^T for one tile: K fragments are read two k-steps ahead of their
   // MFMAs (three rotating sets), so each read has two steps to land.
   // Stage byte offsets are wave-uniform values kept in scalar registers, so
-  // that each fragment address is one add of a per-lane offset plus a
-  // constant in the instruction's offset field.
+  // that each fragment address is one xor of the stage's first fragment
+  // address plus a constant in the instruction's offset field.
   // The fragment addresses of a stage are formed first, made opaque and
   // fenced off from what follows, so that the scheduling groups of the MFMA
   // block below only see the loads, the MFMAs and the softmax.
   auto s_mfma = [&](int st_bytes, f32x16 (&s)[2]) {
     const int sb = __builtin_amdgcn_readfirstlane(st_bytes);
+    const int kb = sb + kofs0;
     int ka[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      ka[ks] = sb + kofs[ks];
+      ka[ks] = kb ^ (32 * ks);
       asm volatile("" : "+v"(ka[ks]));
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -604,10 +626,11 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   // O += V^T P for one tile: transposed V fragments two MFMAs ahead.
   auto pv_mfma = [&](int st_bytes) {
     const int sb = __builtin_amdgcn_readfirstlane(st_bytes);
+    const int vb = sb + vofs0;
     int va4[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      va4[dt] = sb + vofs[dt];
+      va4[dt] = vb ^ (64 * dt);
       asm volatile("" : "+v"(va4[dt]));
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -720,11 +743,139 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
   // of a row: 1560 = 6 x 256 + 24 leaves seven of its eight waves without
   // queries) computes nothing: it issues its share of every tile's loads and
   // the slot lists, and joins every barrier of the schedule below (one after
-  // the slot lists, one in the prologue, one per step), then exits.
+  // the slot lists, one in the prologue, one per step; with PP those of a
+  // group B wave), then exits.
   const bool live = qt * QT + wave * 32 < a.Mq;  // wave-uniform
-  if (!live) {
+  if constexpr (PP) {
+    const bool grpA = wave < 4;
+    // this wave's loads landed, then the barrier
+    auto bar = [&]() {
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    // K/V of tiles 0-2, then one barrier with tiles 0 and 1 landed
+    auto prologue = [&]() {
+      if (live && a.q_ssq) q_lds_load();
+      issue(t_first, 0);
+      if (ntiles > 1) issue(t_first + 1, kAttnStage);
+      if (ntiles > 2) issue(t_first + 2, 2 * kAttnStage);
+      if (ntiles > 2) wait_all_but_one_tile();
+      else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    // right after barrier t: tile t+3 into the stage of tile t-1 (st3),
+    // landed by the issuing wave's next barrier
+    auto issue_next = [&](int t, int st3) {
+      if (t + 3 < ntiles) issue(t_first + t + 3, st3);
+    };
+    if (!live) {
+      // the barriers of a group B wave: the prologue's, barrier 0, one per tile
+      if (ntiles > 0) {
+        prologue();
+        bar();
+        int st3 = 3 * kAttnStage;
+        for (int t = 0; t < ntiles; ++t) {
+          issue_next(t, st3);
+          bar();
+          st3 = st3 == 3 * kAttnStage ? 0 : st3 + kAttnStage;
+        }
+      }
+      return;
+    }
     if (ntiles > 0) {
+      prologue();
+      s_mfma(0, s0);
+      if (a.q_ssq) {
+        // the partials landed with tile 0 (issued before it); read after the barrier
+        asm volatile("" ::: "memory");
+        sc *= q_lds_factor();
+      }
+      if (!grpA) bar();  // B runs one barrier behind A
+      // stages of tiles t, t+1, t+2 and t+3 (= t-1), rotated each tile
+      int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage, st3 = 3 * kAttnStage;
+      auto pstep = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
+        const bool has_next = t + 1 < ntiles;
+        if (!grpA) issue_next(t, st3);
+        float alpha;
+        s_mfma(has_next ? st1 : st0, snxt);
+        const bool moved = softmax(scur, t_first + t, mask_tag, alpha);
+        interleave();
+        asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]));
+        __builtin_amdgcn_sched_barrier(0);
+        if (moved) {
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (grpA) {
+          bar();
+          issue_next(t, st3);
+        }
+        pv_mfma(st0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (!grpA) bar();
+        const int st_done = st0;
+        st0 = st1;
+        st1 = st2;
+        st2 = st3;
+        st3 = st_done;
+      };
+      const std::integral_constant<bool, false> full;
+      const std::integral_constant<bool, true> last;
+      const int nm = ntiles - 1;  // tiles before the last one hold no key past the end
+      int t = 0;
+      for (; t + 1 < nm; t += 2) {
+        pstep(t, s0, s1, full);
+        pstep(t + 1, s1, s0, full);
+      }
+      if (t < nm) {
+        pstep(t, s0, s1, full);
+        pstep(t + 1, s1, s0, last);
+      } else {
+        pstep(t, s0, s1, last);
+      }
+      if (grpA) __builtin_amdgcn_s_barrier();  // B's last barrier
+    }
+  } else {
+    if (!live) {
+      if (ntiles > 0) {
+        if (HIST) {
+          load_slots(t_first, 0);
+          if (ntiles > 1) load_slots(t_first + 1, kAttnStage);
+          if (ntiles > 2) load_slots(t_first + 2, 2 * kAttnStage);
+          __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+        }
+        issue(t_first, 0);
+        if (ntiles > 1) issue(t_first + 1, kAttnStage);
+        if (ntiles > 1) wait_all_but_one_tile();
+        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        __builtin_amdgcn_s_barrier();
+        int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
+        for (int t = 0; t < ntiles; ++t) {
+          const int T = t_first + t;
+          if (t + 1 < ntiles) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+          __builtin_amdgcn_s_barrier();
+          if (HIST) asm volatile("" ::: "memory");
+          if (t + 2 < ntiles) issue(T + 2, st2);
+          if (t + 3 < ntiles) load_slots(T + 3, st0);
+          const int st_done = st0;
+          st0 = st1;
+          st1 = st2;
+          st2 = st_done;
+        }
+      }
+      return;
+    }
+
+    if (ntiles > 0) {
+      // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
+      // tile 0 has landed.
       if (HIST) {
+        // slot lists of the first three tiles, visible to every wave
         load_slots(t_first, 0);
         if (ntiles > 1) load_slots(t_first + 1, kAttnStage);
         if (ntiles > 2) load_slots(t_first + 2, 2 * kAttnStage);
@@ -732,101 +883,68 @@ __global__ __launch_bounds__(64 * NW, 1) void attention_sp_kernel(wam_attention_
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
       }
+      if (a.q_ssq) q_lds_load();
       issue(t_first, 0);
       if (ntiles > 1) issue(t_first + 1, kAttnStage);
       if (ntiles > 1) wait_all_but_one_tile();
       else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
       __builtin_amdgcn_s_barrier();
+      s_mfma(0, s0);
+      if (a.q_ssq) {
+        // the partials landed with tile 0 (issued before it); read after the barrier
+        asm volatile("" ::: "memory");
+        sc *= q_lds_factor();
+      }
+      // Stages of tiles t, t+1 and t+2, rotated each step (scalar values; an
+      // expression in t would become per-lane induction variables).
       int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
-      for (int t = 0; t < ntiles; ++t) {
+      // One step: tile t's softmax under S(t+1) (the last tile's successor is
+      // itself again, computed and discarded), O rescaled where the max moved,
+      // then O += V_t P(t).  Only the last tile is masked.
+      auto step = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
         const int T = t_first + t;
-        if (t + 1 < ntiles) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        const bool has_next = t + 1 < ntiles;
+        // tile t+1 (and the slot list of t+2) has landed and every wave is
+        // done with the stage of t-1 (and with the slot list of t, read two
+        // steps ago)
+        if (has_next) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
         __builtin_amdgcn_s_barrier();
-        if (HIST) asm volatile("" ::: "memory");
+        if (HIST) asm volatile("" ::: "memory");  // slot reads stay below the barrier
         if (t + 2 < ntiles) issue(T + 2, st2);
         if (t + 3 < ntiles) load_slots(T + 3, st0);
+        float alpha;
+        s_mfma(has_next ? st1 : st0, snxt);
+        const bool moved = softmax(scur, T, mask_tag, alpha);
+        interleave();
+        // P(t) is complete here, before the branch below (keeps the
+        // exponentials in this block, between the MFMAs of S(t+1)).
+        asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]));
+        __builtin_amdgcn_sched_barrier(0);
+        if (moved) {
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        }
+        pv_mfma(st0);
+        __builtin_amdgcn_sched_barrier(0);
         const int st_done = st0;
         st0 = st1;
         st1 = st2;
         st2 = st_done;
+      };
+      const std::integral_constant<bool, false> full;
+      const std::integral_constant<bool, true> last;
+      const int nm = ntiles - 1;  // tiles before the last one hold no key past the end
+      int t = 0;
+      for (; t + 1 < nm; t += 2) {
+        step(t, s0, s1, full);
+        step(t + 1, s1, s0, full);
       }
-    }
-    return;
-  }
-
-  if (ntiles > 0) {
-    // Three stages in rotation.  Prologue: tiles 0 and 1 in flight, S(0) once
-    // tile 0 has landed.
-    if (HIST) {
-      // slot lists of the first three tiles, visible to every wave
-      load_slots(t_first, 0);
-      if (ntiles > 1) load_slots(t_first + 1, kAttnStage);
-      if (ntiles > 2) load_slots(t_first + 2, 2 * kAttnStage);
-      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-    }
-    if (a.q_ssq) q_lds_load();
-    issue(t_first, 0);
-    if (ntiles > 1) issue(t_first + 1, kAttnStage);
-    if (ntiles > 1) wait_all_but_one_tile();
-    else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-    __builtin_amdgcn_s_barrier();
-    s_mfma(0, s0);
-    if (a.q_ssq) {
-      // the partials landed with tile 0 (issued before it); read after the barrier
-      asm volatile("" ::: "memory");
-      sc *= q_lds_factor();
-    }
-    // Stages of tiles t, t+1 and t+2, rotated each step (scalar values; an
-    // expression in t would become per-lane induction variables).
-    int st0 = 0, st1 = kAttnStage, st2 = 2 * kAttnStage;
-    // One step: tile t's softmax under S(t+1) (the last tile's successor is
-    // itself again, computed and discarded), O rescaled where the max moved,
-    // then O += V_t P(t).  Only the last tile is masked.
-    auto step = [&](int t, f32x16 (&scur)[2], f32x16 (&snxt)[2], auto mask_tag) {
-      const int T = t_first + t;
-      const bool has_next = t + 1 < ntiles;
-      // tile t+1 (and the slot list of t+2) has landed and every wave is
-      // done with the stage of t-1 (and with the slot list of t, read two
-      // steps ago)
-      if (has_next) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-      __builtin_amdgcn_s_barrier();
-      if (HIST) asm volatile("" ::: "memory");  // slot reads stay below the barrier
-      if (t + 2 < ntiles) issue(T + 2, st2);
-      if (t + 3 < ntiles) load_slots(T + 3, st0);
-      float alpha;
-      s_mfma(has_next ? st1 : st0, snxt);
-      const bool moved = softmax(scur, T, mask_tag, alpha);
-      interleave();
-      // P(t) is complete here, before the branch below (keeps the
-      // exponentials in this block, between the MFMAs of S(t+1)).
-      asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]));
-      __builtin_amdgcn_sched_barrier(0);
-      if (moved) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      if (t < nm) {
+        step(t, s0, s1, full);
+        step(t + 1, s1, s0, last);
+      } else {
+        step(t, s0, s1, last);
       }
-      pv_mfma(st0);
-      __builtin_amdgcn_sched_barrier(0);
-      const int st_done = st0;
-      st0 = st1;
-      st1 = st2;
-      st2 = st_done;
-    };
-    const std::integral_constant<bool, false> full;
-    const std::integral_constant<bool, true> last;
-    const int nm = ntiles - 1;  // tiles before the last one hold no key past the end
-    int t = 0;
-    for (; t + 1 < nm; t += 2) {
-      step(t, s0, s1, full);
-      step(t + 1, s1, s0, full);
-    }
-    if (t < nm) {
-      step(t, s0, s1, full);
-      step(t + 1, s1, s0, last);
-    } else {
-      step(t, s0, s1, last);
     }
   }
 
@@ -924,6 +1042,10 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(wam_attention_ar
 // with the lowest cost whose partials fit in max_bytes wins; no split when
 // none beats the whole-unit grid.  E.g. 4 x 1560 queries over 7800 keys (672
 // units, kt 122): 512 whole + 160 units in 3 ranges, 2.74 vs 3 rounds.
+// Key tiles from which the pipelined kernel runs its ping-pong schedule (8
+// tiles, cross attention over 512 keys, measured 1-3% slower with it).
+constexpr int64_t kAttnPPMinTiles = 16;
+
 struct AttnPlan {
   int n_full, n_split, n_tail, qt;
   double cost;  // in whole-unit times of this plan's units
@@ -1035,8 +1157,13 @@ int attention(const wam_attention_args* a, hipStream_t s) {
   const int QT = query_tile(a, keys);
   const AttnPlan p = attention_plan(a->B, a->Mq, a->H, keys, a->workspace ? a->workspace_bytes : 0, QT);
   const bool hist = a->n_hist_dev != nullptr;
-  auto sp_kernel = QT == 224 ? attention_sp_kernel<false, 7>  // (never with pool keys)
-                             : (hist ? attention_sp_kernel<true, 8> : attention_sp_kernel<false, 8>);
+  // the ping-pong schedule for own keys only, in units of at least
+  // kAttnPPMinTiles key tiles
+  const bool pp = (keys + kAttnKT - 1) / kAttnKT >= kAttnPPMinTiles;
+  auto sp_kernel = QT == 224 ? (pp ? attention_sp_kernel<false, 7, true>  // (never with pool keys)
+                                   : attention_sp_kernel<false, 7, false>)
+                   : hist    ? attention_sp_kernel<true, 8, false>
+                             : (pp ? attention_sp_kernel<false, 8, true> : attention_sp_kernel<false, 8, false>);
   const dim3 sp_block(64 * (QT / 32));
   if (p.n_split > 1) {
     float* part = static_cast<float*>(a->workspace);
