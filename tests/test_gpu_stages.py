@@ -280,7 +280,12 @@ def _ref_attn(q, k, v):
                                        # key, key-range splits (4100 x 4099: 256-query units
                                        # in 3 ranges; 1560 x 7800: 224-query units in 3 ranges)
                                        (2, 1000, 77, 16), (1, 3000, 1, 24), (1, 4100, 4099, 24),
-                                       (3, 700, 2500, 24), (1, 4680, 4680, 24), (1, 1560, 7800, 24)])
+                                       (3, 700, 2500, 24), (1, 4680, 4680, 24), (1, 1560, 7800, 24),
+                                       # the ping-pong schedule (16 key tiles or more) on short
+                                       # key ranges: 256-query units in 8 ranges of 2 tiles;
+                                       # 224-query units in 4 ranges of 4-5 tiles, with a
+                                       # wave past the last query of each row
+                                       (1, 2688, 1024, 25), (2, 1300, 1030, 26)])
 def test_attention_plain(dev, B, Mq, Mk, H):
     from wam_ops import ops
     q = _randn((B, Mq, H, 128), dev, 1)
