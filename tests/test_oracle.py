@@ -205,6 +205,45 @@ def test_fp8_quantization_pinned():
     assert torch.equal(s, (amax.double() / 448.0).float())
 
 
+def test_ffn_gated_pinned():
+    """oracle.fp8.ffn_gated (the FFN unit with its gated residual) against a
+    float64 loop over the definition, with the tanh GELU written out, on
+    shapes where no two dimensions agree (a transposed operand cannot even
+    broadcast), and against the block oracle's own FFN stage (pinned by the
+    reference's golden vectors) for one block of the tiny shape."""
+    from oracle import fp8
+    g = _g(11)
+    M, K, F_, N = 3, 5, 7, 4
+    x = torch.randn(M, K, generator=g)
+    w1, b1 = torch.randn(F_, K, generator=g), torch.randn(F_, generator=g)
+    w2, b2 = torch.randn(N, F_, generator=g), torch.randn(N, generator=g)
+    res, gate = torch.randn(M, N, generator=g), torch.randn(N, generator=g)
+    got = fp8.ffn_gated(x, w1, b1, w2, b2, res, gate).double()
+    c = math.sqrt(2 / math.pi)
+    for m in range(M):
+        h = []
+        for j in range(F_):
+            u = sum(float(x[m, k]) * float(w1[j, k]) for k in range(K)) + float(b1[j])
+            h.append(0.5 * u * (1 + math.tanh(c * (u + 0.044715 * u ** 3))))
+        for n in range(N):
+            y = sum(h[j] * float(w2[n, j]) for j in range(F_)) + float(b2[n])
+            want = float(res[m, n]) + float(gate[n]) * y
+            assert abs(float(got[m, n]) - want) <= 1e-5 * (1 + abs(want)), (m, n)
+    # the FFN stage of the block oracle (fp32): output = residual2 + ffn2 * c_gate
+    from wam_ops import synthetic
+    shape = synthetic.BlockShape(256, 2, 512)
+    params = synthetic.block_params(shape, seed=7)
+    xb, ctx, temb, freqs = synthetic.block_inputs(shape, 1, 24, (2, 3, 4), context_len=8, seed=8)
+    keep = {}
+    out = block_forward(params, xb, ctx, temb, freqs, shape.heads, shape.eps, intermediates=keep)
+    c_gate = keep["modulation"][:, :, 5]
+    unit = fp8.ffn_gated(keep["modulated3"][0], params["ffn.net.0.proj.weight"], params["ffn.net.0.proj.bias"],
+                         params["ffn.net.2.weight"], params["ffn.net.2.bias"], keep["residual2"][0],
+                         c_gate[0, 0])
+    assert (unit - out[0].float()).abs().max() < 1e-4
+    assert (unit - out[0].float()).abs().max() < (out[0].float() - keep["residual2"][0]).abs().max() * 1e-3
+
+
 def test_mx32_quantization_pinned():
     """The oracle's MX (32-value block, e8m0 exponent) quantization: the
     exponent's closed form at the boundaries (448 * 2^X is the largest block
