@@ -406,7 +406,7 @@ def main():
                          "(the workload for the attention instruction-count passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build runs the block on a single MI355X "
+        print("bench.py measures one GPU only: the block runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured path).", file=sys.stderr)
         sys.exit(2)
 

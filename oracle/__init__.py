@@ -1,9 +1,9 @@
 """Oracle: CPU restatement of the reference Wan DiT block.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py may import this package, and only as the checker
-(or, for cpu_baseline, as the timed CPU path that is reported beside the GPU
-number).  The product path (wam_ops) never imports it and has no CPU fallback.
+cpu_baseline leg of bench.py may import this package, and only to check the
+HIP results against it (or, for cpu_baseline, as the timed CPU path that is
+reported beside the GPU number).  The product path (wam_ops) never imports it and has no CPU fallback.
 
 Modules:
   block   - WanTransformerBlock.forward / WanAttention.forward (fp32 or an
